@@ -1,0 +1,66 @@
+"""Build recipe of libfattn.so: hand-written HIP for gfx950 only.
+
+It plays the part of the reference's build.rs (build.rs:5-30), which compiles
+kernels/fused_attn.cu to PTX with nvcc: here hipcc compiles the kernels and the C-ABI layer
+into one shared library holding a gfx950 code object (no PTX, no JIT, no other target).
+
+Usage: ``python candle-fused-attn_amd/build.py`` (or ``build()`` from Python).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+LIB_DIR = PKG_DIR / "lib"
+LIB = LIB_DIR / "libfattn.so"
+SOURCES = [CSRC / "fattn_kernels.hip", CSRC / "fattn_api.cpp"]
+HEADERS = [REPO / "include" / "fattn.h", CSRC / "fattn_internal.h"]
+
+# gfx950 only. Packed fp32 ALU instructions are disabled (-packed-fp32-ops); the host pass warns
+# that it does not know that target feature, which is harmless.
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-mcode-object-version=5",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found: the ROCm toolchain is required to build libfattn.so")
+    return path
+
+
+def command(out: Path = LIB) -> list[str]:
+    return [hipcc(), *HIPCC_FLAGS, f"-I{REPO / 'include'}", f"-I{CSRC}",
+            *[str(s) for s in SOURCES], "-o", str(out)]
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile libfattn.so in-tree (always; the caller decides when to rebuild)."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

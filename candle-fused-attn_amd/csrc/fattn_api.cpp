@@ -1,0 +1,437 @@
+// The C ABI (include/fattn.h): argument validation with the reference's conditions and
+// messages, operand views, workspace layout, and the launches (fattn_kernels.hip).
+//
+// Validation runs before any HIP call, so a rejected call touches no device and needs none.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "fattn.h"
+#include "fattn_internal.h"
+
+namespace fattn {
+
+Workspace workspace_layout(int64_t b, int64_t h, int64_t s) {
+  auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+  Workspace w{};
+  const size_t rows = static_cast<size_t>(b * h * s);
+  const size_t tiles = static_cast<size_t>(b * h * ((s + kBwdQueryTile - 1) / kBwdQueryTile));
+  w.d_off = 0;
+  w.turn_off = up(rows * sizeof(float));
+  w.ctrl_off = w.turn_off + up(tiles * sizeof(int));
+  w.bytes = w.ctrl_off + up(64 * sizeof(int));
+  return w;
+}
+
+}  // namespace fattn
+
+namespace {
+
+using fattn::View;
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int ok() {
+  g_error.clear();
+  return 0;
+}
+
+int hip_fail(int err, const char* what) {
+  g_error = std::string("fused_attention: ") + what + ": " +
+            hipGetErrorString(static_cast<hipError_t>(err));
+  return err;
+}
+
+std::string dims_str(const int64_t* x, int n) {
+  std::string out = "[";
+  for (int i = 0; i < n; ++i) {
+    if (i) out += ", ";
+    out += std::to_string(x[i]);
+  }
+  return out + "]";
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Kernel index range: every (b, h, s) index product and the grid stay inside int32, and the
+// launch inside 2^32 threads.
+int check_range(const char* who, int64_t b, int64_t h, int64_t s) {
+  const int64_t lim = INT32_MAX;
+  if (b > lim || h > lim || s > lim || b * h > lim || b * h * s > lim) {
+    return fail(FATTN_ERANGE, std::string(who) + ": " + std::to_string(b) + " x " +
+                                  std::to_string(h) + " x " + std::to_string(s) +
+                                  " exceeds i32 indexing");
+  }
+  const int64_t grid_lim = (int64_t{1} << 32) / 256 - 1;
+  if (fattn::forward_blocks(b, h, s) > grid_lim || fattn::bwd_main_blocks(b, h, s) > grid_lim ||
+      fattn::bwd_prep_blocks(b, h, s) > grid_lim) {
+    return fail(FATTN_ERANGE, std::string(who) + ": the grid for " + std::to_string(b) +
+                                  " x " + std::to_string(h) + " x " + std::to_string(s) +
+                                  " exceeds the launch limit");
+  }
+  return 0;
+}
+
+int check_head_dim(int64_t d) {
+  if (d != fattn::kHeadDim) {
+    return fail(FATTN_EHEADDIM, "fused_attention: the HIP kernels take head_dim 64, got " +
+                                    std::to_string(d));
+  }
+  return 0;
+}
+
+bool view_aligned(const View& v) {
+  return aligned16(v.p) && v.sb % 4 == 0 && v.sh % 4 == 0 && v.ss % 4 == 0;
+}
+
+View make_view(const float* base, const int64_t st[3]) { return View{base, st[0], st[1], st[2]}; }
+
+// Shared body of the kernel-level forward.
+int run_forward(const char* who, View q, View k, View v, float* o, float* lse, int64_t b,
+                int64_t h, int64_t s, float scale, int causal, void* stream) {
+  if (int rc = check_range(who, b, h, s)) return rc;
+  if (!q.p || !k.p || !v.p || !o || !lse) {
+    return fail(FATTN_EINVAL, std::string(who) + ": null operand");
+  }
+  if (!view_aligned(q) || !view_aligned(k) || !view_aligned(v) || !aligned16(o)) {
+    return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
+  }
+  const int err = fattn::launch_forward(q, k, v, o, lse, static_cast<int>(b),
+                                        static_cast<int>(h), static_cast<int>(s), scale,
+                                        causal ? 1 : 0, stream);
+  if (err) return hip_fail(err, "forward launch");
+  return ok();
+}
+
+struct WsParts {
+  float* dsum;
+  int* turn;
+  int* ctrl;
+};
+
+int workspace_parts(const char* who, void* ws, size_t ws_bytes, int64_t b, int64_t h, int64_t s,
+                    WsParts* out) {
+  const fattn::Workspace l = fattn::workspace_layout(b, h, s);
+  if (!ws || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0 || ws_bytes < l.bytes) {
+    return fail(FATTN_EWORKSPACE, std::string(who) + ": the backward needs a 256-byte aligned " +
+                                      "workspace of " + std::to_string(l.bytes) + " bytes");
+  }
+  char* base = static_cast<char*>(ws);
+  out->dsum = reinterpret_cast<float*>(base + l.d_off);
+  out->turn = reinterpret_cast<int*>(base + l.turn_off);
+  out->ctrl = reinterpret_cast<int*>(base + l.ctrl_off);
+  return 0;
+}
+
+int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_bytes, int64_t b,
+                 int64_t h, int64_t s, void* stream) {
+  if (int rc = check_range(who, b, h, s)) return rc;
+  if (!o || !d_o.p) return fail(FATTN_EINVAL, std::string(who) + ": null operand");
+  if (!aligned16(o) || !view_aligned(d_o)) {
+    return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
+  }
+  WsParts p{};
+  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, &p)) return rc;
+  const int err = fattn::launch_bwd_prep(o, d_o, p.dsum, p.turn, p.ctrl, static_cast<int>(b),
+                                         static_cast<int>(h), static_cast<int>(s), stream);
+  if (err) return hip_fail(err, "backward step 1 launch");
+  return ok();
+}
+
+int run_bwd_main(const char* who, View q, View k, View v, View d_o, const float* lse,
+                 float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h, int64_t s,
+                 float scale, int causal, void* stream) {
+  if (int rc = check_range(who, b, h, s)) return rc;
+  if (!q.p || !k.p || !v.p || !d_o.p || !lse || !dqkv) {
+    return fail(FATTN_EINVAL, std::string(who) + ": null operand");
+  }
+  if (!view_aligned(q) || !view_aligned(k) || !view_aligned(v) || !view_aligned(d_o) ||
+      !aligned16(dqkv)) {
+    return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
+  }
+  WsParts p{};
+  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, &p)) return rc;
+  const int err = fattn::launch_bwd_main(q, k, v, d_o, lse, p.dsum, dqkv, p.turn, p.ctrl,
+                                         static_cast<int>(b), static_cast<int>(h),
+                                         static_cast<int>(s), scale, causal ? 1 : 0, stream);
+  if (err) return hip_fail(err, "backward step 2 launch");
+  return ok();
+}
+
+int run_backward(const char* who, View q, View k, View v, const float* o, View d_o,
+                 const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
+                 int64_t s, float scale, int causal, void* stream) {
+  if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, stream)) return rc;
+  return run_bwd_main(who, q, k, v, d_o, lse, dqkv, ws, ws_bytes, b, h, s, scale, causal,
+                      stream);
+}
+
+bool negative(const int64_t* x, int n) {
+  for (int i = 0; i < n; ++i) {
+    if (x[i] < 0) return true;
+  }
+  return false;
+}
+
+// qkv_geometry (src/lib.rs:191-206): dims (b, heads, s, d); q / k / v view strides
+// [sb, d, ss] at element offsets 0, h d, 2 h d.
+int qkv_geometry(const int64_t shape[3], const int64_t strides[3], int64_t heads, int64_t* b,
+                 int64_t* s, int64_t* d) {
+  if (!shape || !strides || negative(shape, 3) || negative(strides, 3)) {
+    return fail(FATTN_EINVAL, "fused_attention_qkv: a [b, s, 3 h d] layout expected");
+  }
+  const int64_t three_hd = shape[2];
+  if (heads <= 0 || three_hd % (3 * heads) != 0) {
+    return fail(FATTN_EINVAL, "fused_attention_qkv: last dimension " + std::to_string(three_hd) +
+                                  " is not 3 x " + std::to_string(heads) +
+                                  " heads x head_dim");
+  }
+  if (strides[2] != 1 && three_hd > 1) {
+    return fail(FATTN_EINVAL,
+                "fused_attention_qkv: the last dimension must be contiguous, strides " +
+                    dims_str(strides, 3));
+  }
+  *b = shape[0];
+  *s = shape[1];
+  *d = three_hd / 3 / heads;
+  return 0;
+}
+
+// check_shapes + bhs_strides (src/lib.rs:181-220) over q, k, v.
+int bhsd_geometry(const int64_t* qs, const int64_t* qst, const int64_t* ks, const int64_t* kst,
+                  const int64_t* vs, const int64_t* vst) {
+  if (!qs || !qst || !ks || !kst || !vs || !vst || negative(qs, 4) || negative(qst, 4) ||
+      negative(ks, 4) || negative(kst, 4) || negative(vs, 4) || negative(vst, 4)) {
+    return fail(FATTN_EINVAL, "fused_attention: a [b, h, s, d] layout expected");
+  }
+  for (int i = 0; i < 4; ++i) {
+    if (ks[i] != qs[i] || vs[i] != qs[i]) {
+      return fail(FATTN_EINVAL, "fused_attention: q, k, v must share one [b, h, s, d] shape, got " +
+                                    dims_str(qs, 4) + " " + dims_str(ks, 4) + " " +
+                                    dims_str(vs, 4));
+    }
+  }
+  const int64_t* all[3] = {qst, kst, vst};
+  for (const int64_t* st : all) {
+    if (st[3] != 1 && qs[3] > 1) {
+      return fail(FATTN_EINVAL,
+                  "fused_attention: [b, h, s, d] with d contiguous expected, strides " +
+                      dims_str(st, 4));
+    }
+  }
+  return 0;
+}
+
+bool empty3(int64_t b, int64_t h, int64_t s) { return b == 0 || h == 0 || s == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* fattn_last_error(void) { return g_error.c_str(); }
+
+const char* fattn_version(void) { return "fattn-gfx950 0.1.0 (head_dim 64, fp32 MFMA)"; }
+
+size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s) {
+  if (b < 0 || h < 0 || s < 0) return 0;
+  return fattn::workspace_layout(b, h, s).bytes;
+}
+
+int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,
+                      int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
+                      const int64_t q_strides[3], const int64_t k_strides[3],
+                      const int64_t v_strides[3], void* stream) {
+  if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
+  if (int rc = check_head_dim(d)) return rc;
+  if (empty3(b, h, s)) return ok();
+  if (!q_strides || !k_strides || !v_strides) {
+    return fail(FATTN_EINVAL, "fused_attention: null strides");
+  }
+  return run_forward("fused_attention", make_view(q, q_strides), make_view(k, k_strides),
+                     make_view(v, v_strides), o, lse, b, h, s, scale, causal, stream);
+}
+
+int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_strides[3],
+                           void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
+                           int64_t s, int64_t d, void* stream) {
+  if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
+  if (int rc = check_head_dim(d)) return rc;
+  if (empty3(b, h, s)) return ok();
+  if (!do_strides) return fail(FATTN_EINVAL, "fused_attention: null strides");
+  return run_bwd_prep("fused_attention", o, make_view(d_o, do_strides), workspace,
+                      workspace_bytes, b, h, s, stream);
+}
+
+int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
+                           const float* lse, float* dqkv, void* workspace,
+                           size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                           float scale, int causal, const int64_t q_strides[3],
+                           const int64_t k_strides[3], const int64_t v_strides[3],
+                           const int64_t do_strides[3], void* stream) {
+  if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
+  if (int rc = check_head_dim(d)) return rc;
+  if (empty3(b, h, s)) return ok();
+  if (!q_strides || !k_strides || !v_strides || !do_strides) {
+    return fail(FATTN_EINVAL, "fused_attention: null strides");
+  }
+  return run_bwd_main("fused_attention", make_view(q, q_strides), make_view(k, k_strides),
+                      make_view(v, v_strides), make_view(d_o, do_strides), lse, dqkv, workspace,
+                      workspace_bytes, b, h, s, scale, causal, stream);
+}
+
+int fattn_bwd_f32_d64(const float* q, const float* k, const float* v, const float* o,
+                      const float* d_o, const float* lse, float* dqkv, void* workspace,
+                      size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                      float scale, int causal, const int64_t q_strides[3],
+                      const int64_t k_strides[3], const int64_t v_strides[3],
+                      const int64_t do_strides[3], void* stream) {
+  if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
+  if (int rc = check_head_dim(d)) return rc;
+  if (empty3(b, h, s)) return ok();
+  if (!q_strides || !k_strides || !v_strides || !do_strides) {
+    return fail(FATTN_EINVAL, "fused_attention: null strides");
+  }
+  return run_backward("fused_attention", make_view(q, q_strides), make_view(k, k_strides),
+                      make_view(v, v_strides), o, make_view(d_o, do_strides), lse, dqkv,
+                      workspace, workspace_bytes, b, h, s, scale, causal, stream);
+}
+
+int fattn_qkv_forward(const float* qkv, int64_t offset, const int64_t shape[3],
+                      const int64_t strides[3], int64_t heads, float scale, int causal,
+                      float* out, float* lse, void* stream) {
+  int64_t b = 0, s = 0, d = 0;
+  if (int rc = qkv_geometry(shape, strides, heads, &b, &s, &d)) return rc;
+  if (int rc = check_head_dim(d)) return rc;
+  if (empty3(b, heads, s)) return ok();
+  if (!qkv || offset < 0) return fail(FATTN_EINVAL, "fused_attention_qkv: null operand");
+  const int64_t hd = heads * d;
+  const float* base = qkv + offset;
+  if (!aligned16(base) || strides[0] % 4 != 0 || strides[1] % 4 != 0) {
+    return fail(FATTN_EALIGN, "fused_attention_qkv: rows must be 16-byte aligned");
+  }
+  const View q{base, strides[0], d, strides[1]};
+  const View k{base + hd, strides[0], d, strides[1]};
+  const View v{base + 2 * hd, strides[0], d, strides[1]};
+  return run_forward("fused_attention_qkv", q, k, v, out, lse, b, heads, s, scale, causal,
+                     stream);
+}
+
+int fattn_qkv_backward(const float* qkv, int64_t offset, const int64_t shape[3],
+                       const int64_t strides[3], int64_t heads, float scale, int causal,
+                       const float* out, const float* lse, const float* grad,
+                       int64_t grad_offset, const int64_t grad_shape[3],
+                       const int64_t grad_strides[3], float* dqkv, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  int64_t b = 0, s = 0, d = 0;
+  if (int rc = qkv_geometry(shape, strides, heads, &b, &s, &d)) return rc;
+  if (int rc = check_head_dim(d)) return rc;
+  const int64_t hd = heads * d;
+  if (!grad_shape || !grad_strides || grad_shape[0] != b || grad_shape[1] != s ||
+      grad_shape[2] != hd) {
+    const int64_t want[3] = {b, s, hd};
+    return fail(FATTN_EINVAL, "fused_attention_qkv: rank-3 gradient of shape " +
+                                  dims_str(want, 3) + " expected");
+  }
+  if (grad_strides[2] != 1 && hd > 1) {
+    return fail(FATTN_EINVAL, "fused_attention_qkv: the gradient's last dimension must be "
+                              "contiguous, strides " + dims_str(grad_strides, 3));
+  }
+  if (empty3(b, heads, s)) return ok();
+  if (!qkv || !grad || offset < 0 || grad_offset < 0) {
+    return fail(FATTN_EINVAL, "fused_attention_qkv: null operand");
+  }
+  const float* base = qkv + offset;
+  if (!aligned16(base) || strides[0] % 4 != 0 || strides[1] % 4 != 0) {
+    return fail(FATTN_EALIGN, "fused_attention_qkv: rows must be 16-byte aligned");
+  }
+  const View q{base, strides[0], d, strides[1]};
+  const View k{base + hd, strides[0], d, strides[1]};
+  const View v{base + 2 * hd, strides[0], d, strides[1]};
+  const View g{grad + grad_offset, grad_strides[0], d, grad_strides[1]};
+  return run_backward("fused_attention_qkv", q, k, v, out, g, lse, dqkv, workspace,
+                      workspace_bytes, b, heads, s, scale, causal, stream);
+}
+
+int fattn_forward(const float* q, int64_t q_offset, const int64_t q_shape[4],
+                  const int64_t q_strides[4], const float* k, int64_t k_offset,
+                  const int64_t k_shape[4], const int64_t k_strides[4], const float* v,
+                  int64_t v_offset, const int64_t v_shape[4], const int64_t v_strides[4],
+                  float scale, int causal, float* out, float* lse, void* stream) {
+  if (int rc = bhsd_geometry(q_shape, q_strides, k_shape, k_strides, v_shape, v_strides)) {
+    return rc;
+  }
+  if (int rc = check_head_dim(q_shape[3])) return rc;
+  const int64_t b = q_shape[0], h = q_shape[1], s = q_shape[2];
+  if (empty3(b, h, s)) return ok();
+  if (!q || !k || !v || q_offset < 0 || k_offset < 0 || v_offset < 0) {
+    return fail(FATTN_EINVAL, "fused_attention: null operand");
+  }
+  const View qv{q + q_offset, q_strides[0], q_strides[1], q_strides[2]};
+  const View kv{k + k_offset, k_strides[0], k_strides[1], k_strides[2]};
+  const View vv{v + v_offset, v_strides[0], v_strides[1], v_strides[2]};
+  return run_forward("fused_attention", qv, kv, vv, out, lse, b, h, s, scale, causal, stream);
+}
+
+int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
+                   const int64_t q_strides[4], const float* k, int64_t k_offset,
+                   const int64_t k_shape[4], const int64_t k_strides[4], const float* v,
+                   int64_t v_offset, const int64_t v_shape[4], const int64_t v_strides[4],
+                   float scale, int causal, const float* out, const float* lse,
+                   const float* grad, int64_t grad_offset, const int64_t grad_shape[4],
+                   const int64_t grad_strides[4], float* dqkv, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  if (int rc = bhsd_geometry(q_shape, q_strides, k_shape, k_strides, v_shape, v_strides)) {
+    return rc;
+  }
+  if (int rc = check_head_dim(q_shape[3])) return rc;
+  const int64_t b = q_shape[0], h = q_shape[1], s = q_shape[2], d = q_shape[3];
+  // The gradient of the [b, s, h, d] raw output (src/lib.rs:465-475: strides [gb, gs, gh, 1]).
+  if (!grad_shape || !grad_strides || grad_shape[0] != b || grad_shape[1] != s ||
+      grad_shape[2] != h || grad_shape[3] != d) {
+    return fail(FATTN_EINVAL, "fused_attention: rank-4 gradient expected");
+  }
+  if (grad_strides[3] != 1 && d > 1) {
+    return fail(FATTN_EINVAL,
+                "fused_attention: the gradient's last dimension must be contiguous, strides " +
+                    dims_str(grad_strides, 4));
+  }
+  if (empty3(b, h, s)) return ok();
+  if (!q || !k || !v || !grad || q_offset < 0 || k_offset < 0 || v_offset < 0 ||
+      grad_offset < 0) {
+    return fail(FATTN_EINVAL, "fused_attention: null operand");
+  }
+  const View qv{q + q_offset, q_strides[0], q_strides[1], q_strides[2]};
+  const View kv{k + k_offset, k_strides[0], k_strides[1], k_strides[2]};
+  const View vv{v + v_offset, v_strides[0], v_strides[1], v_strides[2]};
+  const View g{grad + grad_offset, grad_strides[0], grad_strides[2], grad_strides[1]};
+  return run_backward("fused_attention", qv, kv, vv, out, g, lse, dqkv, workspace,
+                      workspace_bytes, b, h, s, scale, causal, stream);
+}
+
+int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
+                     int64_t s, void* stream, int* status) {
+  if (!status) return fail(FATTN_EINVAL, "fused_attention: null status");
+  *status = 0;
+  if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
+  WsParts p{};
+  if (int rc = workspace_parts("fused_attention", const_cast<void*>(workspace), workspace_bytes,
+                               b, h, s, &p)) {
+    return rc;
+  }
+  hipError_t err = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return hip_fail(err, "status sync");
+  int guard = 0;
+  err = hipMemcpy(&guard, p.ctrl + fattn::kCtrlGuard, sizeof(int), hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return hip_fail(err, "status copy");
+  *status = guard;
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,55 @@
+// Internal interface between the C-ABI layer (fattn_api.cpp) and the gfx950 kernels
+// (fattn_kernels.hip). Host-only types; no HIP headers needed to include it.
+#ifndef FATTN_INTERNAL_H
+#define FATTN_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fattn {
+
+constexpr int kHeadDim = 64;
+
+// Forward tiling: a workgroup owns kFwdQueries queries of one (batch, head).
+constexpr int kFwdQueries = 64;
+// Backward tiling: a workgroup owns kBwdKeys keys of one (batch, head) and walks query tiles of
+// kBwdQueryTile; one dQ turn counter per query tile.
+constexpr int kBwdKeys = 64;
+constexpr int kBwdQueryTile = 16;
+
+// A [b, h, s, 64] operand on the device: its first element and its (batch, head, seq) strides
+// in floats, head_dim contiguous.
+struct View {
+  const float* p;
+  int64_t sb, sh, ss;
+};
+
+// Workspace of the backward, in this order, each part 256-byte aligned:
+//   D      [b, h, s] f32             rowsum(dO o O)
+//   turn   [b, h, ceil(s / 16)] i32  dQ turn counter per query tile
+//   ctrl   64 i32                    [0] key-block ticket, [32] guard word (spin bound hit)
+struct Workspace {
+  size_t d_off, turn_off, ctrl_off, bytes;
+};
+Workspace workspace_layout(int64_t b, int64_t h, int64_t s);
+constexpr int kCtrlTicket = 0;
+constexpr int kCtrlGuard = 32;
+
+// Launchers (fattn_kernels.hip). They assume validated arguments; they return a hipError_t
+// value as int (0 = launched).
+int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s,
+                   float scale, int causal, void* stream);
+int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl, int b, int h,
+                    int s, void* stream);
+int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
+                    float* dqkv, int* turn, int* ctrl, int b, int h, int s, float scale,
+                    int causal, void* stream);
+
+// Grid sizes the launchers will use (for range checks before launching).
+int64_t forward_blocks(int64_t b, int64_t h, int64_t s);
+int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s);
+int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s);
+
+}  // namespace fattn
+
+#endif  // FATTN_INTERNAL_H

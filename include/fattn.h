@@ -1,0 +1,159 @@
+/*
+ * fattn.h -- the C ABI of the MI355X (gfx950) fused fp32 scaled-dot-product attention,
+ * head_dim 64, forward and deterministic backward.
+ *
+ * This is the drop-in boundary for the reference crate's hot path
+ * (mi-for-the-rust-of-us/candle-fused-attn v0.4.0). Each entry point names the reference
+ * interface it replaces (path:line in that crate). Two levels are exported:
+ *
+ *   - kernel level (replaces the launcher src/cuda.rs and the three kernels of
+ *     kernels/fused_attn.cu): operands are [b, h, s, 64] views given by a base pointer (the
+ *     view's first element) and (batch, head, seq) strides in floats, head_dim contiguous;
+ *   - op level (replaces the candle custom ops' device bodies in src/lib.rs): operands are given
+ *     as a storage pointer, an element offset, a shape and strides, exactly what a candle
+ *     `Layout` holds, and the geometry, shape and alignment checks of src/lib.rs run here.
+ *
+ * Conventions (all entry points):
+ *   - no torch, candle or HIP types in the signatures: `stream` is a hipStream_t passed as
+ *     `void*` (NULL = the null stream);
+ *   - every launch is asynchronous on `stream`; nothing here synchronises the stream, except
+ *     fattn_bwd_status, which says so;
+ *   - outputs are fully written, so they may be uninitialised; nothing is allocated: the
+ *     caller owns O, L, dqkv and the backward workspace;
+ *   - return 0 on success, a negative FATTN_E* code for a rejected argument (nothing is
+ *     launched), or a positive hipError_t for a runtime failure; fattn_last_error() then holds
+ *     a message of this thread prefixed like the reference's (`fused_attention:` or
+ *     `fused_attention_qkv:`);
+ *   - empty inputs (batch, heads or seq 0) are a successful no-op (empty outputs);
+ *   - all arithmetic is fp32; backward results are bit-identical from run to run.
+ */
+#ifndef FATTN_H
+#define FATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The one head dimension the kernels are built for (src/lib.rs:91, CUDA_HEAD_DIM). */
+#define FATTN_HEAD_DIM 64
+
+/* Validation failures (negative return codes). */
+#define FATTN_EINVAL (-1)     /* null pointer, bad rank/shape, non-contiguous last dim, ... */
+#define FATTN_EHEADDIM (-2)   /* head_dim != 64 (src/cuda.rs:85-93) */
+#define FATTN_EALIGN (-3)     /* a row is not 16-byte aligned (src/lib.rs:431-435, :533-538) */
+#define FATTN_ERANGE (-4)     /* a size exceeds the kernels' index or grid range */
+#define FATTN_EWORKSPACE (-5) /* workspace missing, too small or misaligned */
+
+/* ------------------------------------------------------------------------------------------
+ * Kernel level. Replaces src/cuda.rs (forward :139-185, backward :187-260) and the kernels
+ * fattn_fwd_f32_d64 (kernels/fused_attn.cu:469-598), fattn_bwd_dot_f32_d64 (:45-63) and
+ * fattn_bwd_f32_d64 (:213-426). Strides are {batch, head, seq} in floats.
+ * ------------------------------------------------------------------------------------------ */
+
+/* Forward: O [b, s, h, 64] contiguous (the merge-heads layout) and L [b, h, s], the row
+ * log-sum-exp the backward needs. Replaces cuda::forward (src/cuda.rs:139-185). */
+int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,
+                      int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
+                      const int64_t q_strides[3], const int64_t k_strides[3],
+                      const int64_t v_strides[3], void* stream);
+
+/* Bytes of device workspace the backward needs: D = rowsum(dO o O) [b, h, s] f32, the dQ turn
+ * counters and the key-block ticket. Replaces the temporaries cuda::backward allocates
+ * (dsum and turn, src/cuda.rs:200-209). Workspace must be 256-byte aligned. */
+size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s);
+
+/* Backward step 1: D[b, h, i] = sum_c dO[b, i, h, c] * O[b, i, h, c] (fixed order) and the
+ * counters of step 2 cleared. O is [b, s, h, 64] contiguous; dO is read through do_strides.
+ * Replaces the fattn_bwd_dot_f32_d64 launch (src/cuda.rs:215-231). */
+int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_strides[3],
+                           void* workspace, size_t workspace_bytes,
+                           int64_t b, int64_t h, int64_t s, int64_t d, void* stream);
+
+/* Backward step 2: dK, dV and dQ into ONE [b, s, 3, h, 64] buffer (the fused qkv projection's
+ * gradient layout), dQ added in key-block order under per-query-tile turn counters, so every
+ * rerun is bit-identical. Needs step 1 on the same workspace first. Replaces the
+ * fattn_bwd_f32_d64 launch (src/cuda.rs:233-258). */
+int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
+                           const float* lse, float* dqkv, void* workspace,
+                           size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                           float scale, int causal, const int64_t q_strides[3],
+                           const int64_t k_strides[3], const int64_t v_strides[3],
+                           const int64_t do_strides[3], void* stream);
+
+/* Both backward steps. Replaces cuda::backward (src/cuda.rs:187-260). */
+int fattn_bwd_f32_d64(const float* q, const float* k, const float* v, const float* o,
+                      const float* d_o, const float* lse, float* dqkv, void* workspace,
+                      size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                      float scale, int causal, const int64_t q_strides[3],
+                      const int64_t k_strides[3], const int64_t v_strides[3],
+                      const int64_t do_strides[3], void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Op level: the candle custom ops' device bodies. A tensor is (storage, offset, shape,
+ * strides), offset and strides in elements, as in a candle Layout.
+ * ------------------------------------------------------------------------------------------ */
+
+/* softmax(q k^T scale [+ causal mask]) v from a fused [b, s, 3 h d] projection laid out
+ * [q | k | v] along the last dim. out: [b, s, h d] contiguous; lse: [b, h, s] contiguous.
+ * Replaces FusedAttentionQkv::cuda_fwd (src/lib.rs:526-550) with qkv_geometry
+ * (src/lib.rs:191-206). */
+int fattn_qkv_forward(const float* qkv, int64_t offset, const int64_t shape[3],
+                      const int64_t strides[3], int64_t heads, float scale, int causal,
+                      float* out, float* lse, void* stream);
+
+/* The gradient of the projection: dqkv [b, s, 3 h d] contiguous, from the forward's out and
+ * lse and the output gradient grad [b, s, h d] (grad_strides, last one 1). Replaces
+ * FusedAttentionQkv::bwd (src/lib.rs:554-579) and cuda_backward (src/lib.rs:329-366). */
+int fattn_qkv_backward(const float* qkv, int64_t offset, const int64_t shape[3],
+                       const int64_t strides[3], int64_t heads, float scale, int causal,
+                       const float* out, const float* lse, const float* grad,
+                       int64_t grad_offset, const int64_t grad_shape[3],
+                       const int64_t grad_strides[3], float* dqkv, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* Attention over [b, h, s, d] q, k, v with any strides (d contiguous, rows 16-byte aligned).
+ * out: [b, s, h, d] contiguous (the caller's [b, h, s, d] result is its transposed view);
+ * lse: [b, h, s]. Replaces FusedAttention::cuda_fwd (src/lib.rs:420-447) with check_shapes
+ * and bhs_strides (src/lib.rs:181-220). */
+int fattn_forward(const float* q, int64_t q_offset, const int64_t q_shape[4],
+                  const int64_t q_strides[4], const float* k, int64_t k_offset,
+                  const int64_t k_shape[4], const int64_t k_strides[4], const float* v,
+                  int64_t v_offset, const int64_t v_shape[4], const int64_t v_strides[4],
+                  float scale, int causal, float* out, float* lse, void* stream);
+
+/* dQ, dK, dV into one [b, s, 3, h, d] buffer (the caller narrows and transposes it to three
+ * [b, h, s, d] views), from the gradient of the [b, s, h, d] output (grad_shape/grad_strides
+ * in that order). Replaces FusedAttention::bwd (src/lib.rs:449-490). */
+int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
+                   const int64_t q_strides[4], const float* k, int64_t k_offset,
+                   const int64_t k_shape[4], const int64_t k_strides[4], const float* v,
+                   int64_t v_offset, const int64_t v_shape[4], const int64_t v_strides[4],
+                   float scale, int causal, const float* out, const float* lse,
+                   const float* grad, int64_t grad_offset, const int64_t grad_shape[4],
+                   const int64_t grad_strides[4], float* dqkv, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Diagnostics (no counterpart in the reference).
+ * ------------------------------------------------------------------------------------------ */
+
+/* The message of this thread's last failed call ("" if none). */
+const char* fattn_last_error(void);
+
+/* Library version string. */
+const char* fattn_version(void);
+
+/* Synchronises `stream`, then reads the backward's guard word from `workspace` into *status:
+ * 0 = every dQ turn wait ended normally; nonzero = some wait hit its spin bound (the turn
+ * protocol failed, results are invalid). For tests and debugging. */
+int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
+                     int64_t s, void* stream, int* status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FATTN_H */

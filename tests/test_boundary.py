@@ -1,0 +1,199 @@
+"""The C-ABI boundary without a GPU: the library loads, exports every entry point
+include/fattn.h declares, and rejects bad arguments with the reference's conditions and
+messages before touching any device (no compute calls here).
+
+The rejected inputs mirror the reference's own error paths: head_dim != 64 (src/cuda.rs:85-93),
+rows not 16-byte aligned (src/lib.rs:431-435, :533-538), a last dimension not 3 x heads x d
+(src/lib.rs:193-197), a non-contiguous last dimension (src/lib.rs:200-205, :182-187), mismatched
+q/k/v shapes (src/lib.rs:209-219), and the audit's empty-input (B2) and grid-range (B4) cases.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import REPO
+
+import candle_fused_attn as cfa
+from candle_fused_attn import _lib
+
+BAD = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails validation first
+ODD = ctypes.c_void_p(0x1004)   # 4-byte aligned, not 16
+
+
+def header_symbols():
+    text = (REPO / "include" / "fattn.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)  # declarations only, not comments
+    return sorted(set(re.findall(r"\b(fattn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    L = _lib.lib()
+    declared = header_symbols()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(L, name), name
+    assert sorted(_lib.EXPORTS) == declared
+    assert "gfx950" in _lib.version()
+
+
+def a3(*x):
+    return _lib.arr(x)
+
+
+def test_workspace_size_is_aligned_and_monotone():
+    L = _lib.lib()
+    n1 = L.fattn_bwd_workspace_bytes(64, 6, 240)
+    assert n1 % 256 == 0
+    # D (64*6*240 f32) + turns (64*6*15 i32) + control
+    assert n1 >= 64 * 6 * 240 * 4 + 64 * 6 * 15 * 4 + 256
+    assert L.fattn_bwd_workspace_bytes(64, 6, 241) >= n1
+    assert L.fattn_bwd_workspace_bytes(-1, 6, 240) == 0
+
+
+def test_head_dim_gate_before_alignment():
+    L = _lib.lib()
+    st = a3(6 * 24, 6, 3 * 6 * 24 // 1)
+    # qkv with head_dim 6 at a misaligned offset: the head_dim error comes first (audit B3)
+    rc = L.fattn_qkv_forward(BAD, 1, a3(2, 5, 3 * 4 * 6), a3(5 * 72, 72, 1), 4, 0.3, 0, BAD,
+                             BAD, None)
+    assert rc == _lib.FATTN_EHEADDIM
+    assert "head_dim 64, got 6" in _lib.last_error()
+    assert _lib.last_error().startswith("fused_attention")
+    rc = L.fattn_fwd_f32_d64(BAD, BAD, BAD, BAD, BAD, 1, 1, 8, 32, 0.1, 0, st, st, st, None)
+    assert rc == _lib.FATTN_EHEADDIM
+
+
+def test_qkv_geometry_errors():
+    L = _lib.lib()
+    rc = L.fattn_qkv_forward(BAD, 0, a3(2, 5, 100), a3(500, 100, 1), 3, 0.1, 0, BAD, BAD, None)
+    assert rc == _lib.FATTN_EINVAL
+    assert _lib.last_error() == ("fused_attention_qkv: last dimension 100 is not 3 x 3 heads x "
+                                 "head_dim")
+    rc = L.fattn_qkv_forward(BAD, 0, a3(2, 5, 384), a3(1920, 384, 1), 0, 0.1, 0, BAD, BAD, None)
+    assert rc == _lib.FATTN_EINVAL
+    rc = L.fattn_qkv_forward(BAD, 0, a3(2, 5, 384), a3(1920, 384, 2), 2, 0.1, 0, BAD, BAD, None)
+    assert rc == _lib.FATTN_EINVAL
+    assert "last dimension must be contiguous" in _lib.last_error()
+
+
+def test_qkv_alignment_errors():
+    L = _lib.lib()
+    # offset 1, strides aligned
+    rc = L.fattn_qkv_forward(BAD, 1, a3(2, 5, 384), a3(1920, 384, 1), 2, 0.1, 0, BAD, BAD, None)
+    assert rc == _lib.FATTN_EALIGN
+    assert _lib.last_error() == "fused_attention_qkv: rows must be 16-byte aligned"
+    # seq stride not a multiple of 4
+    rc = L.fattn_qkv_forward(BAD, 0, a3(2, 5, 384), a3(1930, 386, 1), 2, 0.1, 0, BAD, BAD, None)
+    assert rc == _lib.FATTN_EALIGN
+    # base pointer misaligned
+    rc = L.fattn_qkv_forward(ODD, 0, a3(2, 5, 384), a3(1920, 384, 1), 2, 0.1, 0, BAD, BAD, None)
+    assert rc == _lib.FATTN_EALIGN
+
+
+def test_general_path_errors():
+    L = _lib.lib()
+    sh, st = a3(2, 3, 5, 64), a3(960, 320, 64, 1)
+    other = a3(2, 3, 6, 64)
+    rc = L.fattn_forward(BAD, 0, sh, st, BAD, 0, other, st, BAD, 0, sh, st, 0.1, 0, BAD, BAD,
+                         None)
+    assert rc == _lib.FATTN_EINVAL
+    assert "must share one [b, h, s, d] shape" in _lib.last_error()
+    rc = L.fattn_forward(BAD, 0, sh, a3(960, 320, 64, 2), BAD, 0, sh, st, BAD, 0, sh, st, 0.1,
+                         0, BAD, BAD, None)
+    assert rc == _lib.FATTN_EINVAL
+    assert "d contiguous expected" in _lib.last_error()
+    rc = L.fattn_forward(BAD, 2, sh, st, BAD, 0, sh, st, BAD, 0, sh, st, 0.1, 0, BAD, BAD, None)
+    assert rc == _lib.FATTN_EALIGN
+    assert _lib.last_error() == "fused_attention: rows must be 16-byte aligned"
+    sh32 = a3(2, 3, 5, 32)
+    rc = L.fattn_forward(BAD, 0, sh32, st, BAD, 0, sh32, st, BAD, 0, sh32, st, 0.1, 0, BAD,
+                         BAD, None)
+    assert rc == _lib.FATTN_EHEADDIM
+
+
+def test_backward_argument_errors():
+    L = _lib.lib()
+    sh, st = a3(2, 5, 384), a3(1920, 384, 1)
+    # gradient of the wrong shape
+    rc = L.fattn_qkv_backward(BAD, 0, sh, st, 2, 0.1, 0, BAD, BAD, BAD, 0, a3(2, 5, 100),
+                              a3(500, 100, 1), BAD, BAD, 1 << 20, None)
+    assert rc == _lib.FATTN_EINVAL
+    assert "rank-3 gradient" in _lib.last_error()
+    # workspace too small
+    rc = L.fattn_qkv_backward(BAD, 0, sh, st, 2, 0.1, 0, BAD, BAD, BAD, 0, a3(2, 5, 128),
+                              a3(640, 128, 1), BAD, ctypes.c_void_p(0x10000), 16, None)
+    assert rc == _lib.FATTN_EWORKSPACE
+    # workspace misaligned
+    rc = L.fattn_qkv_backward(BAD, 0, sh, st, 2, 0.1, 0, BAD, BAD, BAD, 0, a3(2, 5, 128),
+                              a3(640, 128, 1), BAD, ctypes.c_void_p(0x10010), 1 << 20, None)
+    assert rc == _lib.FATTN_EWORKSPACE
+    # general path: gradient of the wrong rank/shape
+    sh4, st4 = a3(2, 3, 5, 64), a3(960, 320, 64, 1)
+    rc = L.fattn_backward(BAD, 0, sh4, st4, BAD, 0, sh4, st4, BAD, 0, sh4, st4, 0.1, 0, BAD,
+                          BAD, BAD, 0, a3(2, 3, 5, 64), a3(960, 192, 64, 1), BAD, BAD, 1 << 20,
+                          None)
+    assert rc == _lib.FATTN_EINVAL
+    assert "rank-4 gradient" in _lib.last_error()
+
+
+def test_empty_inputs_are_a_no_op():
+    """Audit B2: empty inputs give empty outputs on every entry point (no launch, no error)."""
+    L = _lib.lib()
+    for shape in ((0, 5, 384), (2, 0, 384)):
+        rc = L.fattn_qkv_forward(None, 0, a3(*shape), a3(1920, 384, 1), 2, 0.1, 0, None, None,
+                                 None)
+        assert rc == 0, _lib.last_error()
+        rc = L.fattn_qkv_backward(None, 0, a3(*shape), a3(1920, 384, 1), 2, 0.1, 1, None, None,
+                                  None, 0, a3(shape[0], shape[1], 128), a3(640, 128, 1), None,
+                                  None, 0, None)
+        assert rc == 0, _lib.last_error()
+    sh = a3(2, 0, 5, 64)
+    st = a3(960, 320, 64, 1)
+    rc = L.fattn_forward(None, 0, sh, st, None, 0, sh, st, None, 0, sh, st, 0.1, 0, None, None,
+                         None)
+    assert rc == 0
+    rc = L.fattn_fwd_f32_d64(None, None, None, None, None, 0, 3, 7, 64, 0.1, 0, st, st, st,
+                             None)
+    assert rc == 0
+
+
+def test_range_limits():
+    """Audit B4: sizes beyond the kernels' index range are a clean error, not a launch failure."""
+    L = _lib.lib()
+    st = a3(0, 0, 64)
+    rc = L.fattn_fwd_f32_d64(BAD, BAD, BAD, BAD, BAD, 1 << 20, 1 << 8, 1 << 8, 64, 0.1, 0, st,
+                             st, st, None)
+    assert rc == _lib.FATTN_ERANGE
+    assert "exceeds" in _lib.last_error()
+    # 65,536 batches (the reference's gridDim.z limit) is fine here: the grid is one-dimensional
+    ws = L.fattn_bwd_workspace_bytes(65536, 1, 1)
+    assert ws > 0
+
+
+def test_python_api_refuses_cpu_and_non_f32():
+    """No CPU fallback: a CPU tensor or a non-f32 dtype is an error, never a silent path."""
+    x = torch.zeros(2, 5, 384)
+    with pytest.raises(cfa.FusedAttentionError, match="not on a HIP device"):
+        cfa.fused_attention_qkv(x, 2, 0.125, False)
+    q = torch.zeros(2, 2, 5, 64)
+    with pytest.raises(cfa.FusedAttentionError, match="not on a HIP device"):
+        cfa.fused_attention(q, q, q, 0.125, False)
+    with pytest.raises(cfa.FusedAttentionError, match="f32 only"):
+        cfa.fused_attention_qkv(x.double(), 2, 0.125, False)
+
+
+def test_alignment_predicates():
+    qkv = torch.zeros(2, 5, 3 * 2 * 64)
+    assert cfa.reads_in_place(qkv)
+    assert not cfa.reads_in_place(qkv[:, :, 1:])         # offset 1
+    q = qkv.reshape(2, 5, 3, 2, 64)[:, :, 0].transpose(1, 2)  # head view of the projection
+    assert cfa.float4_aligned(q) and cfa.reads_in_place(q)
+    buf = torch.zeros(16, 1024, 16, 64)
+    assert cfa.float4_aligned(buf.transpose(1, 2))       # config 5's views are read in place
+    odd = torch.zeros(2, 3, 5, 66)[..., :64]
+    assert cfa.float4_aligned(odd) is False              # seq stride 66 is not a multiple of 4
+    assert cfa.CUDA_HEAD_DIM == 64
