@@ -323,8 +323,24 @@ struct BwdArgs {
   int causal;
 };
 
-// Spin until the turn counter reads `want` (relaxed polls, then one acquire fence at agent scope,
-// pairing with the releasing key block's fence). Bounded: on timeout the guard word is raised.
+// The dQ hand-over between key blocks. MI355X has one L2 per XCD and the L2s are not coherent
+// with each other, so an agent-scope release / acquire fence pair has to write back / invalidate
+// a whole L2 -- per tile, per workgroup, far more than the 16 x 64 floats that change hands. The
+// hand-over therefore uses accesses that are coherent at agent scope one by one instead: the
+// turn counter and the dQ values are read and written with relaxed agent-scope atomics
+// (global loads / stores with the sc1 scope bit: served at the agent coherence point, not from a
+// stale L2 line), and the writer waits for its dQ stores to complete (vmcnt(0)) before the turn
+// store is issued (after a workgroup barrier, so every wave's stores are complete). A reader
+// issues its dQ loads only after it has seen the turn, so it reads the completed values.
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised.
 __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
   int spins = 0;
   while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) {
@@ -338,7 +354,6 @@ __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
       break;
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
 __global__ void __launch_bounds__(kThreads) bwd_kernel(BwdArgs a) {
@@ -520,7 +535,7 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(BwdArgs a) {
         a.causal ? min(a.nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) : a.nkb - 1;
     if (kb > 0) {
       if (tid == 0) wait_turn(tp + tile, kb, a.ctrl + kCtrlGuard);
-      __syncthreads();  // extends thread 0's acquire to the workgroup
+      __syncthreads();  // no wave reads dQ before the turn is seen
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -529,15 +544,14 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(BwdArgs a) {
         float* dst = a.dqkv + ((static_cast<int64_t>(b) * S + qi) * 3 * a.H + h) * kHeadDim +
                      16 * w + lo;
         float x = dq[r];
-        if (kb > 0) x = *dst + x;
+        if (kb > 0) x = ld_agent(dst) + x;
         if (kb == last) x *= a.scale;
-        *dst = x;
+        st_agent(dst, x);
       }
     }
     if (kb < last) {
-      // Every wave's dQ stores reach the agent coherence point before the turn passes.
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-      __syncthreads();
+      wait_stores();    // this wave's dQ stores are complete at the coherence point
+      __syncthreads();  // ... and every other wave's
       if (tid == 0) __hip_atomic_store(tp + tile, kb + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if (kb == 0) {
       __syncthreads();  // no other barrier this iteration: dS and the staging buffer are reused
