@@ -51,6 +51,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-accuracy", action="store_true", help="skip the fp64 scoring")
     ap.add_argument("--cpu-threads", type=int, default=None)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 256 MiB device-to-device copy (a kernel of known traffic, "
+                         "to scale rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -113,6 +116,13 @@ def main() -> int:
                                             ws_bytes, B, H, S, D, SCALE, ci, qst, qst, qst, gst,
                                             sp))
 
+    if args.calibrate_copy:
+        src = torch.ones(64 * 1024 * 1024, device=dev)   # 256 MiB
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log(f"bench: config {'3 (causal)' if causal else '2'} b{B} h{H} s{S} d{D}; "
         f"warmup {args.warmup}, steps {args.steps}")
     for _ in range(max(args.warmup, 1)):
