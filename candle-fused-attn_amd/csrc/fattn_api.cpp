@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <climits>
 #include <cstdio>
 #include <string>
 
@@ -145,10 +146,21 @@ int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_
   return ok();
 }
 
+// The backward addresses a (b, h) slice of q and dO, and a batch of dqkv, with 32-bit byte or
+// element offsets from a per-slice base.
+bool slice_fits(const View& v, int64_t s) {
+  return (s - 1) * v.ss * 4 + 4 * fattn::kHeadDim <= int64_t{UINT32_MAX};
+}
+
 int run_bwd_main(const char* who, View q, View k, View v, View d_o, const float* lse,
                  float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h, int64_t s,
                  float scale, int causal, void* stream) {
   if (int rc = check_range(who, b, h, s)) return rc;
+  if (!slice_fits(q, s) || !slice_fits(d_o, s) ||
+      s * 3 * h * fattn::kHeadDim > int64_t{UINT32_MAX}) {
+    return fail(FATTN_ERANGE, std::string(who) + ": a (batch, head) slice of " +
+                                  std::to_string(s) + " rows spans more than 4 GiB");
+  }
   if (!q.p || !k.p || !v.p || !d_o.p || !lse || !dqkv) {
     return fail(FATTN_EINVAL, std::string(who) + ": null operand");
   }

@@ -15,7 +15,10 @@ constexpr int kFwdQueries = 64;
 // Backward tiling: a workgroup owns kBwdKeys keys of one (batch, head) and walks query tiles of
 // kBwdQueryTile; one dQ turn counter per query tile.
 constexpr int kBwdKeys = 64;
-constexpr int kBwdQueryTile = 16;
+#ifndef BWD_QT
+#define BWD_QT 16
+#endif
+constexpr int kBwdQueryTile = BWD_QT;
 
 // A [b, h, s, 64] operand on the device: its first element and its (batch, head, seq) strides
 // in floats, head_dim contiguous.
@@ -26,7 +29,7 @@ struct View {
 
 // Workspace of the backward, in this order, each part 256-byte aligned:
 //   D      [b, h, s] f32             rowsum(dO o O)
-//   turn   [b, h, ceil(s / 16)] i32  dQ turn counter per query tile
+//   turn   [b, h, ceil(s / 32)] i32  dQ turn counter per query tile
 //   ctrl   64 i32                    [0] key-block ticket, [32] guard word (spin bound hit)
 struct Workspace {
   size_t d_off, turn_off, ctrl_off, bytes;

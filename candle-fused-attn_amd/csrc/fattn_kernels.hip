@@ -51,6 +51,23 @@ __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<con
 __device__ __forceinline__ void st4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
 __device__ __forceinline__ f4 zero4() { return f4{0.0f, 0.0f, 0.0f, 0.0f}; }
 
+typedef __attribute__((address_space(3))) float lds_float;
+// Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane i's 16 bytes land
+// at `lds_base` + 16 i (M0 holds the wave-uniform LDS address). Completion is counted by vmcnt,
+// like a load; the caller waits (vmcnt(0)) before the barrier that precedes any read of the
+// destination. Written as inline asm so that the compiler, which cannot tell which LDS buffer a
+// copy targets, does not make every later LDS read wait for it (that would serialise the
+// prefetch). M0 is set here and used by nothing else in these kernels. The source is a
+// wave-uniform base (SGPRs) plus a per-lane byte offset below 2^32.
+__device__ __forceinline__ void load_lds16(const float* base, unsigned byte_off, float* lds_base) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_float*)lds_base)));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(byte_off), "s"(base), "s"(lds)
+               : "memory");
+}
+
 // Workgroups are handed to the 8 XCDs round-robin (id % 8). This permutation gives each XCD a
 // contiguous range of logical indices, so logical neighbours (same (b, h)) share one L2.
 __device__ __forceinline__ int xcd_remap(int id, int total) {
@@ -292,24 +309,40 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward, step 2. One workgroup = one key block of 64 keys of one (b, h); wave w owns keys
-// k0 + 16 w .. + 15, one per lane column lo, with K and V of its key in registers (the B operands)
-// and dK^T, dV^T of its keys in accumulators. It walks query tiles of 16 (causal: from the block's
-// first key on), the next tile's Q, dO, L, D in flight during this one (double buffer).
-//   S = Q K^T and dP = dO V^T: M = queries, N = the wave's keys, contraction over d;
-//   A = Q / dO [query lo][dim 16 g + t] (LDS), B = K / V [key lo][dim 16 g + t] (registers).
+// Backward, step 2. One workgroup = one key block of 64 keys of one (b, h), taken by ticket;
+// wave w owns keys k0 + 16 w .. + 15, one per lane column lo, with K and V of its key in registers
+// (the B operands of S and dP), the block's K in the layout of the dQ product's B operand
+// (registers too), and dK^T, dV^T of its keys in accumulators. It walks query tiles of 32 (two
+// 16-query subtiles m; causal: from the block's first key on), the next tile's Q, dO, L, D in
+// flight during this one (LDS double buffer, filled by direct global -> LDS copies).
+//   S = Q K^T and dP = dO V^T per subtile: M = queries, N = the wave's keys, contraction over d;
+//   A = Q / dO [query 16 m + lo][dim 16 g + t] (LDS, float4 reads), B = K / V [key lo][16 g + t].
 //   P = exp(S scale - L), dS = P o (dP - D), in place in the accumulators.
-//   dV^T += dO^T P, dK^T += Q^T dS: M = dims, N = keys, contraction over the tile's queries;
-//   step r uses query 4 g + r, i.e. the P / dS value lane (lo, g) holds in register r.
-//   dQ partial = dS K over the block's 64 keys: dS goes through LDS (the only product that needs
-//   the queries in lo); wave w computes dims 16 w .. + 15, step t contracting keys 4 t + g.
-// The partial is added into dQ on the tile's turn: key block 0 stores, the others read, add and
-// store, the last contributor scales; then the turn passes to the next key block. The tile's dQ
-// is therefore ((p0 + p1) + p2) + ... in key-block order on every run.
+//   dV^T += dO^T P, dK^T += Q^T dS: M = dims, N = keys, contraction over the tile's 32 queries;
+//   step (m, r) uses query 16 m + 4 g + r: the P / dS value lane (lo, g) holds in register r of
+//   subtile m.
+//   dQ partial = dS K over the block's 64 keys: dS goes through LDS (the one product that needs
+//   queries in lo); wave w computes dims 16 w .. + 15, step t contracting keys 16 g + t:
+//   A = dS[16 m + lo][16 g + t] (LDS, float4 reads), B = K[k0 + 16 g + t][16 w + lo] (registers).
+// The partial is added into dQ on the tile's turn, one tile later (software pipelined: while tile
+// t + 1's products run, the loads of what the earlier key blocks summed for tile t are in
+// flight): key block 0 stores, the others add their partial to what they read, the last
+// contributor scales; then the turn passes to the next key block. The tile's dQ is therefore
+// ((p0 + p1) + p2) + ... in key-block order on every run.
 // ---------------------------------------------------------------------------------------------
-constexpr int kQT = kBwdQueryTile;  // 16
-constexpr int kBwdLd = 68;          // Q / dO / dS tile pitch (floats)
-constexpr int kBwdKLd = 80;         // K block pitch: conflict-free reads of K[4 t + g][16 w + lo]
+#ifndef BWD_WAVES
+#define BWD_WAVES 3
+#endif
+constexpr int kQT = kBwdQueryTile;
+constexpr int kNS = kQT / 16;  // 16-query subtiles per tile
+constexpr int kBwdLd = 68;     // dS tile pitch (floats): conflict-free reads and writes
+// Q and dO tiles are [kQT rows][64 floats], unpadded, filled by direct global -> LDS copies; the
+// 16-byte chunk c of row r sits at chunk position c ^ (r % 16), which keeps both read patterns
+// conflict-free: row-wise float4 reads (16 lanes, 16 rows, one chunk each) and column reads
+// (lanes across 4 rows x 16 consecutive floats).
+__device__ __forceinline__ int swz(int row, int col) {
+  return row * kHeadDim + ((((col >> 2) ^ row) & 15) << 2) + (col & 3);
+}
 
 struct BwdArgs {
   View q, k, v, d_o;
@@ -321,11 +354,17 @@ struct BwdArgs {
   int B, H, S, nkb, ntile;
   float scale;
   int causal;
+  int stagger;  // non-causal only: spread the key blocks' walks over the tiles (see below)
 };
+
+// Staggered walks make a key block wait on blocks of its own (b, h) that hold later tickets; that
+// cannot deadlock while all key blocks of one (b, h) can be resident at once, which holds for up
+// to this many per (b, h) on any MI355X partition. Longer sequences use the index order.
+constexpr int kStaggerMaxBlocks = 64;
 
 // The dQ hand-over between key blocks. MI355X has one L2 per XCD and the L2s are not coherent
 // with each other, so an agent-scope release / acquire fence pair has to write back / invalidate
-// a whole L2 -- per tile, per workgroup, far more than the 16 x 64 floats that change hands. The
+// a whole L2 -- per tile, per workgroup, far more than the 32 x 64 floats that change hands. The
 // hand-over therefore uses accesses that are coherent at agent scope one by one instead: the
 // turn counter and the dQ values are read and written with relaxed agent-scope atomics
 // (global loads / stores with the sc1 scope bit: served at the agent coherence point, not from a
@@ -339,6 +378,7 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
 // Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised.
 __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
@@ -356,17 +396,19 @@ __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
   }
 }
 
-__global__ void __launch_bounds__(kThreads) bwd_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(16))) float sQ[2][kQT * kBwdLd];
-  __shared__ __attribute__((aligned(16))) float sdO[2][kQT * kBwdLd];
+// Occupancy target: BWD_WAVES waves per SIMD (the kernel is latency-bound: with fewer, the
+// matrix cores idle behind barriers and the dQ hand-over).
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BWD_WAVES)))
+bwd_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(16))) float sQ[2][kQT * kHeadDim];
+  __shared__ __attribute__((aligned(16))) float sdO[2][kQT * kHeadDim];
   __shared__ __attribute__((aligned(16))) float sdS[kQT * kBwdLd];
-  __shared__ __attribute__((aligned(16))) float sK[kBwdKeys * kBwdKLd];
   __shared__ float sL[2][kQT], sD[2][kQT];
   __shared__ int s_item;
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lo = lane & 15, g = lane >> 4;
-  // Ticket: the key block this workgroup computes, in arrival order. Key block kb of a (b, h) is
-  // item bh * nkb + kb, so the block it waits on (kb - 1) was taken by an earlier, running one.
+  // Ticket: the key block this workgroup computes, in arrival order. Key block kb of a (b, h) has a
+  // later item than kb - 1, so the block it waits on was taken by an earlier, running workgroup.
   if (tid == 0) s_item = atomicAdd(a.ctrl + kCtrlTicket, 1);
   __syncthreads();
   const int item = s_item;
@@ -376,11 +418,17 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(BwdArgs a) {
     if (tid == 0) __hip_atomic_store(a.ctrl + kCtrlGuard, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  const int bh = item / a.nkb, kb = item % a.nkb;
+  // Non-causal: (b, h)-major, the key blocks of one (b, h) adjacent. Causal: key-block-major, so
+  // the expensive low blocks (they see every later query) start first. Either way key block kb
+  // of a (b, h) comes after kb - 1.
+  const int BH = a.B * a.H;
+  const int bh = a.causal ? item % BH : item / a.nkb;
+  const int kb = a.causal ? item / BH : item % a.nkb;
   const int b = bh / a.H, h = bh % a.H, S = a.S;
   const int k0 = kb * kBwdKeys;
   const int kw0 = k0 + 16 * w;  // the wave's first key
   const int key = kw0 + lo;     // this lane's key
+  int* const guard = a.ctrl + kCtrlGuard;
 
   const float* qp = a.q.p + b * a.q.sb + h * a.q.sh;
   const float* kp = a.k.p + b * a.k.sb + h * a.k.sh;
@@ -389,9 +437,19 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(BwdArgs a) {
   const float* lp = a.lse + static_cast<int64_t>(bh) * S;
   const float* dp = a.dsum + static_cast<int64_t>(bh) * S;
   int* tp = a.turn + static_cast<int64_t>(bh) * a.ntile;
+  // Row strides in bytes (the host guarantees every offset within a (b, h) slice < 2^32).
+  const unsigned q_ss4 = static_cast<unsigned>(a.q.ss) * 4u;
+  const unsigned g_ss4 = static_cast<unsigned>(a.d_o.ss) * 4u;
+  // dQ of query qi, dims 16 w + lo: element dq_lane + qi * dq_row of dq_base (part 0 of the
+  // [b, s, 3, h, 64] gradient); the host guarantees s * 3 h * 64 < 2^32.
+  float* const dq_base = a.dqkv + static_cast<int64_t>(b) * S * 3 * a.H * kHeadDim +
+                         static_cast<int64_t>(h) * kHeadDim;
+  const unsigned dq_row = 3u * static_cast<unsigned>(a.H) * kHeadDim;
+  const unsigned dq_lane = 16u * w + lo;
 
-  // B operands of S and dP: K[key][16 g .. 16 g + 15], V likewise.
-  float kB[16], vB[16];
+  // B operands of S and dP: K[key][16 g .. 16 g + 15], V likewise; of the dQ product:
+  // kQ[t] = K[k0 + 16 g + t][16 w + lo]. Zero past S.
+  float kB[16], vB[16], kQ[16];
   if (key < S) {
     const float* kr = kp + key * a.k.ss + 16 * g;
     const float* vr = vp + key * a.v.ss + 16 * g;
@@ -414,42 +472,63 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(BwdArgs a) {
       vB[t] = 0.0f;
     }
   }
-  // The key block's K, for the dQ product; zero rows past S.
-  const int srow = tid >> 4, sc4 = tid & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = srow + 16 * i, kk = k0 + row;
-    const f4 x = kk < S ? ld4(kp + kk * a.k.ss + 4 * sc4) : zero4();
-    st4(&sK[row * kBwdKLd + 4 * sc4], x);
+  for (int t = 0; t < 16; ++t) {
+    const int kk = k0 + 16 * g + t;
+    kQ[t] = kk < S ? kp[kk * a.k.ss + 16 * w + lo] : 0.0f;
   }
 
-  // Staging of one query tile: thread tid moves Q and dO row tid / 16, float4 column tid % 16;
-  // threads 0..15 move L, 16..31 move D. Zero past S.
-  f4 qst = zero4(), gst = zero4();
+  // Staging of one query tile: wave w copies Q and dO rows kQT / 4 * w .. + kQT / 4 - 1 with
+  // direct copies of four rows each (lane i: row + i / 16, chunk position i % 16, i.e. logical
+  // chunk (i % 16) ^ row); rows past S repeat row S - 1 (finite, masked later). Threads
+  // 0..kQT-1 load L, kQT..2 kQT-1 load D into a register (zero past S), written by sstore.
   float lst = 0.0f;
-  auto gload = [&](int q0) {
-    const int qq = q0 + srow;
-    if (qq < S) {
-      qst = ld4(qp + qq * a.q.ss + 4 * sc4);
-      gst = ld4(gp + qq * a.d_o.ss + 4 * sc4);
-    } else {
-      qst = zero4();
-      gst = zero4();
+  auto gload = [&](int q0, float* Qdst, float* Gdst) {
+#pragma unroll
+    for (int j = 0; j < kQT / 16; ++j) {
+      const int row0 = (kQT / 4) * w + 4 * j;
+      const int row = row0 + (lane >> 4);
+      const unsigned qq = static_cast<unsigned>(min(q0 + row, S - 1));
+      const unsigned c4 = 16u * static_cast<unsigned>((lane & 15) ^ (row & 15));
+      load_lds16(qp, qq * q_ss4 + c4, Qdst + row0 * kHeadDim);
+      load_lds16(gp, qq * g_ss4 + c4, Gdst + row0 * kHeadDim);
     }
-    if (tid < 16) {
+    if (tid < kQT) {
       lst = q0 + tid < S ? lp[q0 + tid] : 0.0f;
-    } else if (tid < 32) {
-      lst = q0 + tid - 16 < S ? dp[q0 + tid - 16] : 0.0f;
+    } else if (tid < 2 * kQT) {
+      lst = q0 + tid - kQT < S ? dp[q0 + tid - kQT] : 0.0f;
     }
   };
   auto sstore = [&](int buf) {
-    st4(&sQ[buf][srow * kBwdLd + 4 * sc4], qst);
-    st4(&sdO[buf][srow * kBwdLd + 4 * sc4], gst);
-    if (tid < 16) {
+    if (tid < kQT) {
       sL[buf][tid] = lst;
-    } else if (tid < 32) {
-      sD[buf][tid - 16] = lst;
+    } else if (tid < 2 * kQT) {
+      sD[buf][tid - kQT] = lst;
     }
+  };
+  // The order in which key blocks add into a tile's dQ (fixed by the shape alone, so every run
+  // sums in the same order), chosen so that a block's predecessor reaches the tile first:
+  //   causal: blocks 0 .. last (those holding a key <= the tile's last query), in index order;
+  //     block kb walks tiles upward from its first key, after the lower blocks (ticket order);
+  //   non-causal: block kb walks all tiles starting at t0(kb) = kb ntile / nkb (wrapping), so the
+  //     blocks are spread over the tiles; tile j's order is the order in which the blocks reach it
+  //     in that walk: kb* (the last block with t0 <= j) first, then kb* - 1, ..., 0, then
+  //     nkb - 1, ..., kb* + 1. Its predecessor is then about ntile / nkb tiles ahead of it.
+  //     (Without `stagger`: every block walks from tile 0 and the order is 0 .. nkb - 1.)
+  // pos_of: this block's position in tile j's order; count_of: the number of contributors.
+  const int t0 = a.causal ? k0 / kQT : (a.stagger ? (kb * a.ntile) / a.nkb : 0);
+  const int nsteps = a.causal ? a.ntile - t0 : a.ntile;
+  auto tile_at = [&](int step) {
+    const int j = t0 + step;
+    return a.causal ? j : (j >= a.ntile ? j - a.ntile : j);
+  };
+  auto pos_of = [&](int j) {
+    if (a.causal || !a.stagger) return kb;
+    const int kstar = min(a.nkb - 1, (j * a.nkb + a.nkb - 1) / a.ntile);
+    return kstar >= kb ? kstar - kb : kstar - kb + a.nkb;
+  };
+  auto count_of = [&](int j) {
+    return a.causal ? min(a.nkb - 1, min(S - 1, j * kQT + kQT - 1) / kBwdKeys) + 1 : a.nkb;
   };
 
   f4 dva[4], dka[4];
@@ -458,104 +537,188 @@ __global__ void __launch_bounds__(kThreads) bwd_kernel(BwdArgs a) {
     dva[mt] = zero4();
     dka[mt] = zero4();
   }
-
-  // Causal: queries before the block's first key see none of its keys.
-  const int q_begin = a.causal ? k0 : 0;
-  gload(q_begin);
-  sstore(0);
-  __syncthreads();
-  for (int t = 0, q0 = q_begin; q0 < S; ++t, q0 += kQT) {
-    const int buf = t & 1;
-    const bool has_next = q0 + kQT < S;
-    if (has_next) gload(q0 + kQT);
-    const float* Qt = sQ[buf];
-    const float* Gt = sdO[buf];
-    // Wave-uniform liveness of each wave's 16 keys for this tile (all masked: skip the math).
-    int live_mask = 0;
+  // The dQ hand-over runs two tiles behind the products (software pipelined):
+  //   stage 1 (iteration j + 1): wait for tile j's turn, load what the earlier key blocks summed
+  //     -- in flight during that iteration's products;
+  //   stage 2 (iteration j + 2): add this block's partial, store -- the stores complete during
+  //     that iteration's products, before its first barrier, after which the turn passes.
+  // p1: partial computed, sums not yet loaded; p2: sums loaded, not yet stored. For each: the
+  // tile's first query (-1: none), this block's position in the tile's order, the contributors.
+  int p1_q0 = -1, p1_pos = 0, p1_cnt = 1, p2_q0 = -1, p2_pos = 0, p2_cnt = 1;
+  f4 p1[kNS], p2[kNS];
+  float p1s[kNS][4], p2s[kNS][4];
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      const int kx = k0 + 16 * ww;
-      if (kx < S && !(a.causal && kx > q0 + kQT - 1)) live_mask |= 1 << ww;
+  for (int m = 0; m < kNS; ++m) {
+    p1[m] = zero4();
+    p2[m] = zero4();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p1s[m][r] = 0.0f;
+      p2s[m][r] = 0.0f;
     }
-
-    f4 dS = zero4();
-    if (live_mask & (1 << w)) {
-      f4 sS = zero4(), sP = zero4();
-      const float* qr = Qt + lo * kBwdLd + 16 * g;
-      const float* gr = Gt + lo * kBwdLd + 16 * g;
+  }
+  // Stage 1 for the tile at q0p: this wave waits for the turn (one lane polls), then loads.
+  auto load_sums = [&](int q0p, int pos, float (&sums)[kNS][4]) {
+    if (pos == 0) return;
+    if (lane == 0) wait_turn(tp + q0p / kQT, pos, guard);
+    compiler_fence();
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const f4 x = ld4(qr + 4 * u), y = ld4(gr + 4 * u);
-        sS = mma(x.x, kB[4 * u], sS);
-        sS = mma(x.y, kB[4 * u + 1], sS);
-        sS = mma(x.z, kB[4 * u + 2], sS);
-        sS = mma(x.w, kB[4 * u + 3], sS);
-        sP = mma(y.x, vB[4 * u], sP);
-        sP = mma(y.y, vB[4 * u + 1], sP);
-        sP = mma(y.z, vB[4 * u + 2], sP);
-        sP = mma(y.w, vB[4 * u + 3], sP);
-      }
-      // Lane (lo, g), register r: query q0 + 4 g + r, key `key`.
-      f4 P;
+    for (int m = 0; m < kNS; ++m) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int il = 4 * g + r, qi = q0 + il;
-        const bool ok = qi < S && key < S && !(a.causal && key > qi);
-        P[r] = ok ? exp2_hw(fmaf(sS[r], a.scale, -sL[buf][il]) * kLog2e) : 0.0f;
-        dS[r] = P[r] * (sP[r] - sD[buf][il]);
+        const int qi = q0p + 16 * m + 4 * g + r;
+        sums[m][r] = qi < S ? ld_agent(dq_base + (dq_lane + qi * dq_row)) : 0.0f;
       }
+    }
+  };
+  // Stage 2: the running sum plus this block's partial (x scale by the last contributor).
+  auto store_sums = [&](int q0p, int pos, int cnt, const f4 (&part)[kNS],
+                        const float (&sums)[kNS][4]) {
+#pragma unroll
+    for (int m = 0; m < kNS; ++m) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float* grow = Gt + (4 * g + r) * kBwdLd + lo;
-        const float* qrow = Qt + (4 * g + r) * kBwdLd + lo;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          dva[mt] = mma(grow[16 * mt], P[r], dva[mt]);
-          dka[mt] = mma(qrow[16 * mt], dS[r], dka[mt]);
+        const int qi = q0p + 16 * m + 4 * g + r;
+        if (qi < S) {
+          float x = pos > 0 ? sums[m][r] + part[m][r] : part[m][r];
+          if (pos == cnt - 1) x *= a.scale;
+          st_agent(dq_base + (dq_lane + qi * dq_row), x);
         }
       }
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sdS[(4 * g + r) * kBwdLd + 16 * w + lo] = dS[r];
-    __syncthreads();
-
-    // dQ partial for dims 16 w + lo; step t4 contracts keys 4 t4 + g (keys of wave t4 / 4).
-    f4 dq = zero4();
-#pragma unroll
-    for (int t4 = 0; t4 < 16; ++t4) {
-      if (!(live_mask & (1 << (t4 >> 2)))) continue;
-      const int kl = 4 * t4 + g;
-      dq = mma(sdS[lo * kBwdLd + kl], sK[kl * kBwdKLd + 16 * w + lo], dq);
+  };
+  // After stage 2's stores completed (vmcnt(0) and a barrier): the next contributor's turn.
+  auto pass_turn = [&](int q0p, int pos, int cnt) {
+    if (pos + 1 < cnt && tid == 0) {
+      __hip_atomic_store(tp + q0p / kQT, pos + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (has_next) sstore(buf ^ 1);  // that buffer's last readers passed the previous barrier
+  };
 
-    // Ordered accumulation of the tile's dQ over key blocks 0 .. last.
-    const int tile = q0 / kQT;
-    const int last =
-        a.causal ? min(a.nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) : a.nkb - 1;
-    if (kb > 0) {
-      if (tid == 0) wait_turn(tp + tile, kb, a.ctrl + kCtrlGuard);
-      __syncthreads();  // no wave reads dQ before the turn is seen
-    }
+  // Causal: the walk starts at the block's first key (earlier queries see none of its keys).
+  gload(tile_at(0) * kQT, sQ[0], sdO[0]);
+  sstore(0);
+  wait_stores();  // the direct copies have landed
+  __syncthreads();
+  for (int t = 0; t < nsteps; ++t) {
+    const int buf = t & 1;
+    const int q0 = tile_at(t) * kQT;
+    const bool has_next = t + 1 < nsteps;
+    // The next tile into the other buffer, whose last readers passed the last barrier.
+    if (has_next) gload(tile_at(t + 1) * kQT, sQ[buf ^ 1], sdO[buf ^ 1]);
+    const float* Qt = sQ[buf];
+    const float* Gt = sdO[buf];
+    if (p2_q0 >= 0) store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);  // stage 2, two tiles back
+
+    // Wave-uniform liveness of each 16-query subtile for this wave's 16 keys.
+    bool live[kNS];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int qi = q0 + 4 * g + r;
-      if (qi < S) {
-        float* dst = a.dqkv + ((static_cast<int64_t>(b) * S + qi) * 3 * a.H + h) * kHeadDim +
-                     16 * w + lo;
-        float x = dq[r];
-        if (kb > 0) x = ld_agent(dst) + x;
-        if (kb == last) x *= a.scale;
-        st_agent(dst, x);
+    for (int m = 0; m < kNS; ++m) {
+      const int qm0 = q0 + 16 * m;
+      live[m] = qm0 < S && kw0 < S && !(a.causal && kw0 > qm0 + 15);
+    }
+
+    // S and dP.
+    f4 sS[kNS], sP[kNS];
+#pragma unroll
+    for (int m = 0; m < kNS; ++m) {
+      sS[m] = zero4();
+      sP[m] = zero4();
+      if (!live[m]) continue;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int at = swz(16 * m + lo, 16 * g + 4 * u);
+        const f4 x = ld4(Qt + at), y = ld4(Gt + at);
+        sS[m] = mma(x.x, kB[4 * u], sS[m]);
+        sS[m] = mma(x.y, kB[4 * u + 1], sS[m]);
+        sS[m] = mma(x.z, kB[4 * u + 2], sS[m]);
+        sS[m] = mma(x.w, kB[4 * u + 3], sS[m]);
+        sP[m] = mma(y.x, vB[4 * u], sP[m]);
+        sP[m] = mma(y.y, vB[4 * u + 1], sP[m]);
+        sP[m] = mma(y.z, vB[4 * u + 2], sP[m]);
+        sP[m] = mma(y.w, vB[4 * u + 3], sP[m]);
       }
     }
-    if (kb < last) {
-      wait_stores();    // this wave's dQ stores are complete at the coherence point
-      __syncthreads();  // ... and every other wave's
-      if (tid == 0) __hip_atomic_store(tp + tile, kb + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else if (kb == 0) {
-      __syncthreads();  // no other barrier this iteration: dS and the staging buffer are reused
+
+    if (p1_q0 >= 0) load_sums(p1_q0, p1_pos, p1s);  // stage 1, one tile back
+
+    // P = exp(S scale - L), dS = P o (dP - D); lane (lo, g), register r of subtile m: query
+    // q0 + 16 m + 4 g + r, key `key`. Then dV^T and dK^T.
+#pragma unroll
+    for (int m = 0; m < kNS; ++m) {
+      if (!live[m]) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int il = 16 * m + 4 * g + r, qi = q0 + il;
+        const bool ok = qi < S && key < S && !(a.causal && key > qi);
+        const float p = ok ? exp2_hw(fmaf(sS[m][r], a.scale, -sL[buf][il]) * kLog2e) : 0.0f;
+        sP[m][r] = p * (sP[m][r] - sD[buf][il]);  // dS
+        sS[m][r] = p;                              // P
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const int at = swz(16 * m + 4 * g + r, 16 * mt + lo);
+          dva[mt] = mma(Gt[at], sS[m][r], dva[mt]);
+          dka[mt] = mma(Qt[at], sP[m][r], dka[mt]);
+        }
+      }
     }
+
+    // This tile's dS into LDS (zero where the wave's keys are all masked).
+#pragma unroll
+    for (int m = 0; m < kNS; ++m) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sdS[(16 * m + 4 * g + r) * kBwdLd + 16 * w + lo] = sP[m][r];
+    }
+    wait_stores();    // stage 2's stores, stage 1's loads and the next tile's copies complete
+    __syncthreads();  // dS complete; every wave's stage-2 stores complete
+    if (p2_q0 >= 0) pass_turn(p2_q0, p2_pos, p2_cnt);
+
+    // Stages advance; this tile's dQ partial enters stage 1.
+    p2_q0 = p1_q0;
+    p2_pos = p1_pos;
+    p2_cnt = p1_cnt;
+#pragma unroll
+    for (int m = 0; m < kNS; ++m) {
+      p2[m] = p1[m];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p2s[m][r] = p1s[m][r];
+    }
+#pragma unroll
+    for (int m = 0; m < kNS; ++m) {
+      p1[m] = zero4();
+      if (q0 + 16 * m >= S) continue;
+      const float* sr = sdS + (16 * m + lo) * kBwdLd + 16 * g;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f4 x = ld4(sr + 4 * u);
+        p1[m] = mma(x.x, kQ[4 * u], p1[m]);
+        p1[m] = mma(x.y, kQ[4 * u + 1], p1[m]);
+        p1[m] = mma(x.z, kQ[4 * u + 2], p1[m]);
+        p1[m] = mma(x.w, kQ[4 * u + 3], p1[m]);
+      }
+    }
+    p1_q0 = q0;
+    p1_pos = pos_of(q0 / kQT);
+    p1_cnt = count_of(q0 / kQT);
+    if (has_next) sstore(buf ^ 1);
+    __syncthreads();  // dS read by every wave; the next tile's L and D staged
+  }
+
+  // Drain: the two tiles still in the pipeline, in order.
+  if (p2_q0 >= 0) {
+    store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);
+    wait_stores();
+    __syncthreads();
+    pass_turn(p2_q0, p2_pos, p2_cnt);
+  }
+  if (p1_q0 >= 0) {
+    load_sums(p1_q0, p1_pos, p1s);
+    store_sums(p1_q0, p1_pos, p1_cnt, p1, p1s);
+    wait_stores();
+    __syncthreads();
+    pass_turn(p1_q0, p1_pos, p1_cnt);
   }
 
   // dK (x scale) and dV of this lane's key: dims 16 mt + 4 g .. + 3, one float4 each.
@@ -604,8 +767,9 @@ int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl,
 int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
                     float* dqkv, int* turn, int* ctrl, int b, int h, int s, float scale,
                     int causal, void* stream) {
+  const int nkb = (s + kBwdKeys - 1) / kBwdKeys;
   BwdArgs a{q, k, v, d_o, lse, dsum, dqkv, turn, ctrl, b, h, s,
-            (s + kBwdKeys - 1) / kBwdKeys, (s + kQT - 1) / kQT, scale, causal};
+            nkb, (s + kQT - 1) / kQT, scale, causal, !causal && nkb <= kStaggerMaxBlocks ? 1 : 0};
   void* args[] = {&a};
   return static_cast<int>(hipLaunchKernel(reinterpret_cast<const void*>(bwd_kernel),
                                           dim3(static_cast<unsigned>(bwd_main_blocks(b, h, s))),

@@ -413,3 +413,19 @@ def test_config5_strided_views_large_logits(orc, cuda):
     dq, dk, dv = (t.grad.transpose(1, 2).cpu().numpy() for t in leaves)
     check_sampled(orc, qn, kn, vn, do.numpy(), o.detach().cpu().numpy(), dq, dk, dv, 0.125,
                   False, sample_slices(16, 16, 6, 5), "config5")
+
+
+@pytest.mark.parametrize("s", [4096, 4160])
+def test_long_sequences_both_walk_orders(orc, cuda, s):
+    """Non-causal key blocks walk staggered over the tiles up to 64 blocks per (b, h) (s 4096)
+    and in index order beyond (s 4160): both against fp64, and bit-identical reruns."""
+    rng = np.random.default_rng(s)
+    x = rng.standard_normal((1, s, 3 * 64)).astype(np.float32)
+    w = rng.standard_normal((1, s, 64)).astype(np.float32)
+    say(f"long non-causal s{s}")
+    ref_out, _, ref_grad = oracle_qkv(orc, x, w, 1, 64, False, np.float64, 0.125)
+    qkv, wt = torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda)
+    out, grad = run("fused_qkv", qkv, wt, 1, 64, False, 0.125)
+    check_errors(orc, out, grad, ref_out, ref_grad, f"s{s}")
+    _, grad2 = run("fused_qkv", qkv, wt, 1, 64, False, 0.125)
+    assert torch.equal(bits(grad), bits(grad2))
