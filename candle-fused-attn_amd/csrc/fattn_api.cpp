@@ -71,7 +71,7 @@ int check_range(const char* who, int64_t b, int64_t h, int64_t s) {
                                   " exceeds i32 indexing");
   }
   const int64_t grid_lim = (int64_t{1} << 32) / 256 - 1;
-  if (fattn::forward_blocks(b, h, s) > grid_lim || fattn::bwd_main_blocks(b, h, s) > grid_lim ||
+  if (fattn::forward_blocks(b, h, s, 1) > grid_lim || fattn::bwd_main_blocks(b, h, s) > grid_lim ||
       fattn::bwd_prep_blocks(b, h, s) > grid_lim) {
     return fail(FATTN_ERANGE, std::string(who) + ": the grid for " + std::to_string(b) +
                                   " x " + std::to_string(h) + " x " + std::to_string(s) +
@@ -94,6 +94,17 @@ bool view_aligned(const View& v) {
 
 View make_view(const float* base, const int64_t st[3]) { return View{base, st[0], st[1], st[2]}; }
 
+// The kernels address a (b, h) slice of an operand (and a batch of dqkv) with 32-bit byte or
+// element offsets from a per-slice base.
+bool slice_fits(const View& v, int64_t s) {
+  return (s - 1) * v.ss * 4 + 4 * fattn::kHeadDim <= int64_t{UINT32_MAX};
+}
+
+int slice_error(const char* who, int64_t s) {
+  return fail(FATTN_ERANGE, std::string(who) + ": a (batch, head) slice of " + std::to_string(s) +
+                                " rows spans more than 4 GiB");
+}
+
 // Shared body of the kernel-level forward.
 int run_forward(const char* who, View q, View k, View v, float* o, float* lse, int64_t b,
                 int64_t h, int64_t s, float scale, int causal, void* stream) {
@@ -104,6 +115,7 @@ int run_forward(const char* who, View q, View k, View v, float* o, float* lse, i
   if (!view_aligned(q) || !view_aligned(k) || !view_aligned(v) || !aligned16(o)) {
     return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
   }
+  if (!slice_fits(k, s) || !slice_fits(v, s)) return slice_error(who, s);
   const int err = fattn::launch_forward(q, k, v, o, lse, static_cast<int>(b),
                                         static_cast<int>(h), static_cast<int>(s), scale,
                                         causal ? 1 : 0, stream);
@@ -146,20 +158,13 @@ int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_
   return ok();
 }
 
-// The backward addresses a (b, h) slice of q and dO, and a batch of dqkv, with 32-bit byte or
-// element offsets from a per-slice base.
-bool slice_fits(const View& v, int64_t s) {
-  return (s - 1) * v.ss * 4 + 4 * fattn::kHeadDim <= int64_t{UINT32_MAX};
-}
-
 int run_bwd_main(const char* who, View q, View k, View v, View d_o, const float* lse,
                  float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h, int64_t s,
                  float scale, int causal, void* stream) {
   if (int rc = check_range(who, b, h, s)) return rc;
   if (!slice_fits(q, s) || !slice_fits(d_o, s) ||
       s * 3 * h * fattn::kHeadDim > int64_t{UINT32_MAX}) {
-    return fail(FATTN_ERANGE, std::string(who) + ": a (batch, head) slice of " +
-                                  std::to_string(s) + " rows spans more than 4 GiB");
+    return slice_error(who, s);
   }
   if (!q.p || !k.p || !v.p || !d_o.p || !lse || !dqkv) {
     return fail(FATTN_EINVAL, std::string(who) + ": null operand");

@@ -10,8 +10,6 @@ namespace fattn {
 
 constexpr int kHeadDim = 64;
 
-// Forward tiling: a workgroup owns kFwdQueries queries of one (batch, head).
-constexpr int kFwdQueries = 64;
 // Backward tiling: a workgroup owns kBwdKeys keys of one (batch, head) and walks query tiles of
 // kBwdQueryTile; one dQ turn counter per query tile.
 constexpr int kBwdKeys = 64;
@@ -49,7 +47,7 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const fl
                     int causal, void* stream);
 
 // Grid sizes the launchers will use (for range checks before launching).
-int64_t forward_blocks(int64_t b, int64_t h, int64_t s);
+int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal);
 int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s);
 int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s);
 

@@ -76,23 +76,51 @@ __device__ __forceinline__ int xcd_remap(int id, int total) {
   return (id & 7) * (full >> 3) + (id >> 3);
 }
 
+// Waits until every vector memory operation of this wave has completed (loads returned, stores
+// and direct copies landed).
+__device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Tiles staged by direct copies are [rows][64 floats], unpadded; the 16-byte chunk c of row r
+// sits at chunk position c ^ (r % 16), which keeps both read patterns used on them
+// conflict-free: row-wise float4 reads (16 lanes, 16 rows, one chunk each) and column reads
+// (lanes across 4 rows x 16 consecutive floats).
+__device__ __forceinline__ int swz(int row, int col) {
+  return row * kHeadDim + ((((col >> 2) ^ row) & 15) << 2) + (col & 3);
+}
+
+// Copy rows [row0, row0 + 4 n) of a [rows][64] tile from global (base + row * row_bytes, rows past
+// `last` repeat row `last`) into the swizzled LDS tile `dst`, n direct copies of 4 rows per wave:
+// lane i moves chunk position i % 16 of row row0 + 4 j + i / 16, i.e. logical chunk
+// (i % 16) ^ row.
+template <int N>
+__device__ __forceinline__ void copy_rows(const float* base, unsigned row_bytes, int first_row,
+                                          int last_row, float* dst, int row0, int lane) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int row = row0 + 4 * j + (lane >> 4);
+    const unsigned src_row = static_cast<unsigned>(min(first_row + row, last_row));
+    const unsigned c16 = 16u * static_cast<unsigned>((lane & 15) ^ (row & 15));
+    load_lds16(base, src_row * row_bytes + c16, dst + (row0 + 4 * j) * kHeadDim);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
-// Forward. One workgroup = 64 queries of one (b, h); wave w owns queries q0 + 16 w .. + 15, one
-// per lane column lo. Key tiles of 64 are staged in LDS (double buffered, the next tile's loads in
-// flight during this tile's math) and shared by the four waves.
-//   S^T = K Q^T per 16-key subtile: A = K[key 16 mt + lo][dim 16 g + t] (LDS, float4 reads),
-//   B = Q[query lo][dim 16 g + t] (registers, loaded once). Output: lane (lo, g) holds
-//   S[query lo][key 16 mt + 4 g + r].
+// Forward. One workgroup = 4 waves x kFwdWaveQ queries of one (b, h) (QB in all); wave w owns
+// queries q0 + kFwdWaveQ w .., in kFwdNT column tiles of 16 (one query per lane column lo each).
+// Key tiles of KT keys are staged in LDS by direct copies (double buffered: the next tile's
+// copies in flight during this tile's math) and shared by the four waves. Two shapes are built
+// (measured on MI355X): non-causal QB 128 / KT 32 (each K / V operand read from LDS serves two
+// query tiles), causal QB 64 / KT 48 (smaller blocks balance the triangular work better).
+//   S^T = K Q^T per 16-key subtile and column tile n: A = K[key 16 mt + lo][dim 16 g + t] (LDS,
+//   float4 reads, shared by the column tiles), B = Q[query lo][dim 16 g + t] (registers, loaded
+//   once). Output: lane (lo, g) holds S[query lo][key 16 mt + 4 g + r].
 //   O^T += V^T P^T: M = dims (four 16-row tiles), N = queries, contraction over the tile's keys;
 //   step (kt, r) uses key 16 kt + 4 g + r, i.e. exactly the P value lane (lo, g) holds in its
-//   register (kt, r). A = V[key][dim 16 mt + lo] (LDS).
+//   register (kt, r). A = V[key][dim 16 mt + lo] (LDS, shared by the column tiles).
 // Online softmax per query: running max m (identical in the four lanes of the query), running
 // partial sum over the lane's own keys (combined across the four lanes once, in a fixed order,
 // at the end), O rescaled by alpha = exp(m_old - m_new) when the max grows.
 // ---------------------------------------------------------------------------------------------
-constexpr int kFwdWaveQ = 16;
-constexpr int kFwdKeys = 64;
-constexpr int kFwdLd = 68;  // LDS row pitch (floats): conflict-free float4 and column reads
 
 struct FwdArgs {
   View q, k, v;
@@ -103,9 +131,16 @@ struct FwdArgs {
   int causal;
 };
 
-__global__ void __launch_bounds__(kThreads) fwd_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(16))) float sK[2][kFwdKeys * kFwdLd];
-  __shared__ __attribute__((aligned(16))) float sV[2][kFwdKeys * kFwdLd];
+template <int QB, int KT>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+fwd_kernel(FwdArgs a) {
+  constexpr int kFwdQueries = QB;          // queries per workgroup
+  constexpr int kFwdWaveQ = QB / 4;        // queries per wave
+  constexpr int kFwdNT = kFwdWaveQ / 16;   // 16-query column tiles per wave
+  constexpr int kFwdKeys = KT;             // keys per LDS tile
+  constexpr int kFwdSub = KT / 16;         // 16-key subtiles per tile
+  __shared__ __attribute__((aligned(16))) float sK[2][kFwdKeys * kHeadDim];
+  __shared__ __attribute__((aligned(16))) float sV[2][kFwdKeys * kHeadDim];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lo = lane & 15, g = lane >> 4;
   const int S = a.S, BH = a.B * a.H;
@@ -122,26 +157,32 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(FwdArgs a) {
   const int b = bh / a.H, h = bh % a.H;
   const int q0 = qb * kFwdQueries;
   const int qw0 = q0 + w * kFwdWaveQ;  // the wave's first query
-  const int qi = qw0 + lo;             // this lane's query
   const float* qp = a.q.p + b * a.q.sb + h * a.q.sh;
   const float* kp = a.k.p + b * a.k.sb + h * a.k.sh;
   const float* vp = a.v.p + b * a.v.sb + h * a.v.sh;
+  // Row strides in bytes (the host guarantees every offset within a (b, h) slice < 2^32).
+  const unsigned k_ss4 = static_cast<unsigned>(a.k.ss) * 4u;
+  const unsigned v_ss4 = static_cast<unsigned>(a.v.ss) * 4u;
 
-  // B operand of S^T: Q[qi][16 g .. 16 g + 15].
-  float qr[16];
-  if (qi < S) {
-    const float* r = qp + qi * a.q.ss + 16 * g;
+  // B operands of S^T: Q[qi(n)][16 g .. 16 g + 15] for this lane's query in column tile n.
+  float qr[kFwdNT][16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const f4 x = ld4(r + 4 * u);
-      qr[4 * u] = x.x;
-      qr[4 * u + 1] = x.y;
-      qr[4 * u + 2] = x.z;
-      qr[4 * u + 3] = x.w;
+  for (int n = 0; n < kFwdNT; ++n) {
+    const int qi = qw0 + 16 * n + lo;
+    if (qi < S) {
+      const float* r = qp + qi * a.q.ss + 16 * g;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f4 x = ld4(r + 4 * u);
+        qr[n][4 * u] = x.x;
+        qr[n][4 * u + 1] = x.y;
+        qr[n][4 * u + 2] = x.z;
+        qr[n][4 * u + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) qr[n][t] = 0.0f;
     }
-  } else {
-#pragma unroll
-    for (int t = 0; t < 16; ++t) qr[t] = 0.0f;
   }
 
   // Keys the block needs, and keys this wave's rows can see.
@@ -150,125 +191,126 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(FwdArgs a) {
   const int kw_end = a.causal ? min(S, qw0 + kFwdWaveQ) : S;
   const bool wave_live = qw0 < S;
 
-  // Staging: thread tid moves rows (tid / 16) + 16 i, float4 column tid % 16, of K and V.
-  const int srow = tid >> 4, sc4 = tid & 15;
-  f4 kst[4], vst[4];
-  auto gload = [&](int kt0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = kt0 + srow + 16 * i;
-      if (key < S) {
-        kst[i] = ld4(kp + key * a.k.ss + 4 * sc4);
-        vst[i] = ld4(vp + key * a.v.ss + 4 * sc4);
-      } else {  // zero rows: masked scores, and 0 * V must stay 0
-        kst[i] = zero4();
-        vst[i] = zero4();
-      }
-    }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      st4(&sK[buf][(srow + 16 * i) * kFwdLd + 4 * sc4], kst[i]);
-      st4(&sV[buf][(srow + 16 * i) * kFwdLd + 4 * sc4], vst[i]);
-    }
+  // Staging: wave w copies K and V rows kFwdKeys / 4 * w .. + kFwdKeys / 4 - 1 of the tile; keys
+  // past S repeat key S - 1 (finite; their scores are masked, so 0 * V stays 0).
+  auto stage = [&](int kt0, int buf) {
+    copy_rows<kFwdKeys / 16>(kp, k_ss4, kt0, S - 1, sK[buf], (kFwdKeys / 4) * w, lane);
+    copy_rows<kFwdKeys / 16>(vp, v_ss4, kt0, S - 1, sV[buf], (kFwdKeys / 4) * w, lane);
   };
 
-  f4 acc[4];
+  f4 acc[kFwdNT][4];
+  float m[kFwdNT], lsum[kFwdNT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) acc[mt] = zero4();
-  float m = kNegInf, lsum = 0.0f;
+  for (int n = 0; n < kFwdNT; ++n) {
+    m[n] = kNegInf;
+    lsum[n] = 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[n][mt] = zero4();
+  }
 
-  gload(0);
-  sstore(0);
+  stage(0, 0);
+  wait_mem();
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1, kt0 = t * kFwdKeys;
-    const bool has_next = t + 1 < ntiles;
-    if (has_next) gload(kt0 + kFwdKeys);  // in flight during this tile's math
+    // The next tile into the other buffer, whose last readers passed the last barrier.
+    if (t + 1 < ntiles) stage(kt0 + kFwdKeys, buf ^ 1);
     if (wave_live) {
       const float* Kt = sK[buf];
       const float* Vt = sV[buf];
-      bool live[4];
+      bool live[kFwdSub];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) live[mt] = kt0 + 16 * mt < kw_end;  // wave-uniform
-      f4 s[4];
+      for (int mt = 0; mt < kFwdSub; ++mt) live[mt] = kt0 + 16 * mt < kw_end;  // wave-uniform
+      f4 s[kFwdNT][kFwdSub];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        s[mt] = zero4();
+      for (int mt = 0; mt < kFwdSub; ++mt) {
+#pragma unroll
+        for (int n = 0; n < kFwdNT; ++n) s[n][mt] = zero4();
         if (live[mt]) {
-          const float* kr = Kt + (16 * mt + lo) * kFwdLd + 16 * g;
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const f4 kk = ld4(kr + 4 * u);
-            s[mt] = mma(kk.x, qr[4 * u], s[mt]);
-            s[mt] = mma(kk.y, qr[4 * u + 1], s[mt]);
-            s[mt] = mma(kk.z, qr[4 * u + 2], s[mt]);
-            s[mt] = mma(kk.w, qr[4 * u + 3], s[mt]);
+            const f4 kk = ld4(Kt + swz(16 * mt + lo, 16 * g + 4 * u));
+#pragma unroll
+            for (int n = 0; n < kFwdNT; ++n) {
+              s[n][mt] = mma(kk.x, qr[n][4 * u], s[n][mt]);
+              s[n][mt] = mma(kk.y, qr[n][4 * u + 1], s[n][mt]);
+              s[n][mt] = mma(kk.z, qr[n][4 * u + 2], s[n][mt]);
+              s[n][mt] = mma(kk.w, qr[n][4 * u + 3], s[n][mt]);
+            }
           }
         }
       }
-      // Scale, mask (keys past S; causal keys after the query), tile max.
-      float tmax = kNegInf;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int n = 0; n < kFwdNT; ++n) {
+        const int qi = qw0 + 16 * n + lo;
+        // Scale, mask (keys past S; causal keys after the query), tile max.
+        float tmax = kNegInf;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kt0 + 16 * mt + 4 * g + r;
-          const bool ok = live[mt] && key < S && !(a.causal && key > qi);
-          const float x = ok ? s[mt][r] * a.scale : kNegInf;
-          s[mt][r] = x;
-          tmax = fmaxf(tmax, x);
+        for (int mt = 0; mt < kFwdSub; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = kt0 + 16 * mt + 4 * g + r;
+            const bool ok = live[mt] && key < S && !(a.causal && key > qi);
+            const float x = ok ? s[n][mt][r] * a.scale : kNegInf;
+            s[n][mt][r] = x;
+            tmax = fmaxf(tmax, x);
+          }
         }
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float m_new = fmaxf(m, tmax);
-      // A row with every key so far masked keeps m = -inf (exp(-inf - -inf) would be NaN).
-      const bool none = m_new == kNegInf;
-      const float alpha = none ? 1.0f : exp2_hw((m - m_new) * kLog2e);
-      float psum = 0.0f;
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m[n], tmax);
+        // A row with every key so far masked keeps m = -inf (exp(-inf - -inf) would be NaN).
+        const bool none = m_new == kNegInf;
+        const float alpha = none ? 1.0f : exp2_hw((m[n] - m_new) * kLog2e);
+        float psum = 0.0f;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < kFwdSub; ++mt) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = none ? 0.0f : exp2_hw((s[mt][r] - m_new) * kLog2e);
-          s[mt][r] = p;
-          psum += p;
+          for (int r = 0; r < 4; ++r) {
+            const float p = none ? 0.0f : exp2_hw((s[n][mt][r] - m_new) * kLog2e);
+            s[n][mt][r] = p;
+            psum += p;
+          }
         }
+        lsum[n] = lsum[n] * alpha + psum;
+        m[n] = m_new;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[n][mt] *= alpha;
       }
-      lsum = lsum * alpha + psum;
-      m = m_new;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) acc[mt] *= alpha;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < kFwdSub; ++kt) {
         if (!live[kt]) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float* vr = Vt + (16 * kt + 4 * g + r) * kFwdLd + lo;
-          const float p = s[kt][r];
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt) acc[mt] = mma(vr[16 * mt], p, acc[mt]);
+          for (int mt = 0; mt < 4; ++mt) {
+            const float vv = Vt[swz(16 * kt + 4 * g + r, 16 * mt + lo)];
+#pragma unroll
+            for (int n = 0; n < kFwdNT; ++n) acc[n][mt] = mma(vv, s[n][kt][r], acc[n][mt]);
+          }
         }
       }
     }
-    if (has_next) sstore(buf ^ 1);  // that buffer's last readers passed the previous barrier
-    __syncthreads();
+    wait_mem();       // the next tile's copies have landed
+    __syncthreads();  // and every wave is done with this tile's buffers
   }
 
   if (wave_live) {
-    // The row sum: the four lanes of a query hold partial sums over disjoint keys; every lane
-    // adds them in the same order.
-    const float l0 = __shfl(lsum, lo), l1 = __shfl(lsum, lo + 16);
-    const float l2 = __shfl(lsum, lo + 32), l3 = __shfl(lsum, lo + 48);
-    const float l = (l0 + l1) + (l2 + l3);
-    if (qi < S) {
-      const float inv = 1.0f / l;
-      float* orow = a.o + ((static_cast<int64_t>(b) * S + qi) * a.H + h) * kHeadDim;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) st4(orow + 16 * mt + 4 * g, acc[mt] * inv);
-      if (g == 0) a.lse[static_cast<int64_t>(bh) * S + qi] = m + logf(l);
+    for (int n = 0; n < kFwdNT; ++n) {
+      // The row sum: the four lanes of a query hold partial sums over disjoint keys; every lane
+      // adds them in the same order.
+      const float l0 = __shfl(lsum[n], lo), l1 = __shfl(lsum[n], lo + 16);
+      const float l2 = __shfl(lsum[n], lo + 32), l3 = __shfl(lsum[n], lo + 48);
+      const float l = (l0 + l1) + (l2 + l3);
+      const int qi = qw0 + 16 * n + lo;
+      if (qi < S) {
+        const float inv = 1.0f / l;
+        float* orow = a.o + ((static_cast<int64_t>(b) * S + qi) * a.H + h) * kHeadDim;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) st4(orow + 16 * mt + 4 * g, acc[n][mt] * inv);
+        if (g == 0) a.lse[static_cast<int64_t>(bh) * S + qi] = m[n] + logf(l);
+      }
     }
   }
 }
@@ -336,13 +378,7 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
 constexpr int kQT = kBwdQueryTile;
 constexpr int kNS = kQT / 16;  // 16-query subtiles per tile
 constexpr int kBwdLd = 68;     // dS tile pitch (floats): conflict-free reads and writes
-// Q and dO tiles are [kQT rows][64 floats], unpadded, filled by direct global -> LDS copies; the
-// 16-byte chunk c of row r sits at chunk position c ^ (r % 16), which keeps both read patterns
-// conflict-free: row-wise float4 reads (16 lanes, 16 rows, one chunk each) and column reads
-// (lanes across 4 rows x 16 consecutive floats).
-__device__ __forceinline__ int swz(int row, int col) {
-  return row * kHeadDim + ((((col >> 2) ^ row) & 15) << 2) + (col & 3);
-}
+// Q and dO tiles are [kQT rows][64 floats] in the swizzled layout of swz(), filled by direct copies.
 
 struct BwdArgs {
   View q, k, v, d_o;
@@ -377,7 +413,7 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 __device__ __forceinline__ void st_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_stores() { wait_mem(); }
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
 // Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised.
@@ -484,15 +520,8 @@ bwd_kernel(BwdArgs a) {
   // 0..kQT-1 load L, kQT..2 kQT-1 load D into a register (zero past S), written by sstore.
   float lst = 0.0f;
   auto gload = [&](int q0, float* Qdst, float* Gdst) {
-#pragma unroll
-    for (int j = 0; j < kQT / 16; ++j) {
-      const int row0 = (kQT / 4) * w + 4 * j;
-      const int row = row0 + (lane >> 4);
-      const unsigned qq = static_cast<unsigned>(min(q0 + row, S - 1));
-      const unsigned c4 = 16u * static_cast<unsigned>((lane & 15) ^ (row & 15));
-      load_lds16(qp, qq * q_ss4 + c4, Qdst + row0 * kHeadDim);
-      load_lds16(gp, qq * g_ss4 + c4, Gdst + row0 * kHeadDim);
-    }
+    copy_rows<kQT / 16>(qp, q_ss4, q0, S - 1, Qdst, (kQT / 4) * w, lane);
+    copy_rows<kQT / 16>(gp, g_ss4, q0, S - 1, Gdst, (kQT / 4) * w, lane);
     if (tid < kQT) {
       lst = q0 + tid < S ? lp[q0 + tid] : 0.0f;
     } else if (tid < 2 * kQT) {
@@ -736,8 +765,13 @@ bwd_kernel(BwdArgs a) {
 
 }  // namespace
 
-int64_t forward_blocks(int64_t b, int64_t h, int64_t s) {
-  return ((s + kFwdQueries - 1) / kFwdQueries) * h * b;
+// The two forward shapes: queries per workgroup, keys per tile.
+constexpr int kFwdQB[2] = {128, 64};  // [causal]
+constexpr int kFwdKT[2] = {32, 48};
+
+int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal) {
+  const int qb = kFwdQB[causal ? 1 : 0];
+  return ((s + qb - 1) / qb) * h * b;
 }
 int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s) {
   return ((s + kBwdKeys - 1) / kBwdKeys) * h * b;
@@ -746,10 +780,13 @@ int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s) { return (b * h * s + 1
 
 int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s,
                    float scale, int causal, void* stream) {
-  FwdArgs a{q, k, v, o, lse, b, h, s, (s + kFwdQueries - 1) / kFwdQueries, scale, causal};
+  const int c = causal ? 1 : 0;
+  FwdArgs a{q, k, v, o, lse, b, h, s, (s + kFwdQB[c] - 1) / kFwdQB[c], scale, c};
   void* args[] = {&a};
-  return static_cast<int>(hipLaunchKernel(reinterpret_cast<const void*>(fwd_kernel),
-                                          dim3(static_cast<unsigned>(forward_blocks(b, h, s))),
+  const void* fn = c ? reinterpret_cast<const void*>(fwd_kernel<kFwdQB[1], kFwdKT[1]>)
+                     : reinterpret_cast<const void*>(fwd_kernel<kFwdQB[0], kFwdKT[0]>);
+  return static_cast<int>(hipLaunchKernel(fn,
+                                          dim3(static_cast<unsigned>(forward_blocks(b, h, s, c))),
                                           dim3(kThreads), args, 0,
                                           static_cast<hipStream_t>(stream)));
 }

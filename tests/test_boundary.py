@@ -197,3 +197,14 @@ def test_alignment_predicates():
     odd = torch.zeros(2, 3, 5, 66)[..., :64]
     assert cfa.float4_aligned(odd) is False              # seq stride 66 is not a multiple of 4
     assert cfa.CUDA_HEAD_DIM == 64
+
+
+def test_slice_offsets_must_fit_32_bits():
+    """The kernels address one (batch, head) slice with 32-bit offsets: a slice spanning more
+    than 4 GiB is refused up front (no launch)."""
+    L = _lib.lib()
+    st = a3(0, 0, 1 << 28)   # seq stride 2^28 floats = 1 GiB per row
+    ok = a3(0, 0, 64)
+    rc = L.fattn_fwd_f32_d64(BAD, BAD, BAD, BAD, BAD, 1, 1, 8, 64, 0.1, 0, ok, st, ok, None)
+    assert rc == _lib.FATTN_ERANGE
+    assert "4 GiB" in _lib.last_error()
