@@ -415,6 +415,13 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
 }
 __device__ __forceinline__ void wait_stores() { wait_mem(); }
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+// Vector memory operations complete in issue order (vmcnt counts them down in order), so this
+// waits for everything but the last kStage1Loads operations issued: stage 1's loads.
+constexpr int kStage1Loads = 4 * kNS;
+static_assert(kStage1Loads == 4, "wait_except_stage1 encodes vmcnt(4)");
+__device__ __forceinline__ void wait_except_stage1() {
+  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+}
 
 // Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised.
 __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
@@ -587,6 +594,9 @@ bwd_kernel(BwdArgs a) {
     }
   }
   // Stage 1 for the tile at q0p: this wave waits for the turn (one lane polls), then loads.
+  // Exactly kStage1Loads load instructions are issued (rows past S read row S - 1, unused), the
+  // last vector memory operations before the iteration's first barrier, so that barrier need not
+  // wait for them (see wait_except_stage1).
   auto load_sums = [&](int q0p, int pos, float (&sums)[kNS][4]) {
     if (pos == 0) return;
     if (lane == 0) wait_turn(tp + q0p / kQT, pos, guard);
@@ -595,10 +605,11 @@ bwd_kernel(BwdArgs a) {
     for (int m = 0; m < kNS; ++m) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int qi = q0p + 16 * m + 4 * g + r;
-        sums[m][r] = qi < S ? ld_agent(dq_base + (dq_lane + qi * dq_row)) : 0.0f;
+        const int qi = min(q0p + 16 * m + 4 * g + r, S - 1);
+        sums[m][r] = ld_agent(dq_base + (dq_lane + qi * dq_row));
       }
     }
+    compiler_fence();
   };
   // Stage 2: the running sum plus this block's partial (x scale by the last contributor).
   auto store_sums = [&](int q0p, int pos, int cnt, const f4 (&part)[kNS],
@@ -637,6 +648,7 @@ bwd_kernel(BwdArgs a) {
     const float* Qt = sQ[buf];
     const float* Gt = sdO[buf];
     if (p2_q0 >= 0) store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);  // stage 2, two tiles back
+    compiler_fence();
 
     // Wave-uniform liveness of each 16-query subtile for this wave's 16 keys.
     bool live[kNS];
@@ -700,7 +712,13 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) sdS[(16 * m + 4 * g + r) * kBwdLd + 16 * w + lo] = sP[m][r];
     }
-    wait_stores();    // stage 2's stores, stage 1's loads and the next tile's copies complete
+    // Stage 2's stores and the next tile's copies complete (stage 1's loads, issued last, may
+    // still be in flight: they are needed only in the next iteration).
+    if (p1_q0 >= 0 && p1_pos > 0) {
+      wait_except_stage1();
+    } else {
+      wait_mem();
+    }
     __syncthreads();  // dS complete; every wave's stage-2 stores complete
     if (p2_q0 >= 0) pass_turn(p2_q0, p2_pos, p2_cnt);
 
