@@ -597,9 +597,9 @@ bwd_kernel(BwdArgs a) {
   // Exactly kStage1Loads load instructions are issued (rows past S read row S - 1, unused), the
   // last vector memory operations before the iteration's first barrier, so that barrier need not
   // wait for them (see wait_except_stage1).
-  auto load_sums = [&](int q0p, int pos, float (&sums)[kNS][4]) {
+  auto load_sums = [&](int q0p, int pos, int seen, float (&sums)[kNS][4]) {
     if (pos == 0) return;
-    if (lane == 0) wait_turn(tp + q0p / kQT, pos, guard);
+    if (lane == 0 && seen != pos) wait_turn(tp + q0p / kQT, pos, guard);
     compiler_fence();
 #pragma unroll
     for (int m = 0; m < kNS; ++m) {
@@ -647,6 +647,12 @@ bwd_kernel(BwdArgs a) {
     if (has_next) gload(tile_at(t + 1) * kQT, sQ[buf ^ 1], sdO[buf ^ 1]);
     const float* Qt = sQ[buf];
     const float* Gt = sdO[buf];
+    // Stage 1's turn, read early (one lane, no wait here): by the time it is checked below the
+    // value has arrived, and usually the turn with it.
+    int seen = -1;
+    if (p1_q0 >= 0 && p1_pos > 0 && lane == 0) {
+      seen = __hip_atomic_load(tp + p1_q0 / kQT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (p2_q0 >= 0) store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);  // stage 2, two tiles back
     compiler_fence();
 
@@ -680,7 +686,7 @@ bwd_kernel(BwdArgs a) {
       }
     }
 
-    if (p1_q0 >= 0) load_sums(p1_q0, p1_pos, p1s);  // stage 1, one tile back
+    if (p1_q0 >= 0) load_sums(p1_q0, p1_pos, seen, p1s);  // stage 1, one tile back
 
     // P = exp(S scale - L), dS = P o (dP - D); lane (lo, g), register r of subtile m: query
     // q0 + 16 m + 4 g + r, key `key`. Then dV^T and dK^T.
@@ -761,7 +767,7 @@ bwd_kernel(BwdArgs a) {
     pass_turn(p2_q0, p2_pos, p2_cnt);
   }
   if (p1_q0 >= 0) {
-    load_sums(p1_q0, p1_pos, p1s);
+    load_sums(p1_q0, p1_pos, -1, p1s);
     store_sums(p1_q0, p1_pos, p1_cnt, p1, p1s);
     wait_stores();
     __syncthreads();
