@@ -12,6 +12,7 @@ from .ops import (
     fused_attention,
     fused_attention_qkv,
     reads_in_place,
+    set_dq_sum,
 )
 
 __all__ = [
@@ -23,5 +24,6 @@ __all__ = [
     "fused_attention",
     "fused_attention_qkv",
     "reads_in_place",
+    "set_dq_sum",
     "version",
 ]

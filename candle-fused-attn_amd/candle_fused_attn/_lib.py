@@ -23,6 +23,8 @@ FATTN_EWORKSPACE = -5
 EXPORTS = (
     "fattn_fwd_f32_d64",
     "fattn_bwd_workspace_bytes",
+    "fattn_bwd_workspace_min_bytes",
+    "fattn_bwd_workspace_split_bytes",
     "fattn_bwd_prep_f32_d64",
     "fattn_bwd_main_f32_d64",
     "fattn_bwd_f32_d64",
@@ -60,8 +62,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.fattn_last_error.restype = ctypes.c_char_p
     L.fattn_version.argtypes = []
     L.fattn_version.restype = ctypes.c_char_p
-    L.fattn_bwd_workspace_bytes.argtypes = [I64, I64, I64]
-    L.fattn_bwd_workspace_bytes.restype = SIZE
+    for name in ("fattn_bwd_workspace_bytes", "fattn_bwd_workspace_min_bytes",
+                 "fattn_bwd_workspace_split_bytes"):
+        getattr(L, name).argtypes = [I64, I64, I64]
+        getattr(L, name).restype = SIZE
     L.fattn_fwd_f32_d64.argtypes = [P, P, P, P, P, I64, I64, I64, I64, C_FLOAT, C_INT, A3, A3,
                                     A3, P]
     L.fattn_bwd_prep_f32_d64.argtypes = [P, P, A3, P, SIZE, I64, I64, I64, I64, P]
@@ -78,7 +82,7 @@ def _declare(L: ctypes.CDLL) -> None:
                                  P, P, P, I64, A3, A3, P, P, SIZE, P]
     L.fattn_bwd_status.argtypes = [P, SIZE, I64, I64, I64, P, ctypes.POINTER(C_INT)]
     for name in EXPORTS:
-        if name not in ("fattn_last_error", "fattn_version", "fattn_bwd_workspace_bytes"):
+        if name not in ("fattn_last_error", "fattn_version") and "workspace" not in name:
             getattr(L, name).restype = C_INT
 
 

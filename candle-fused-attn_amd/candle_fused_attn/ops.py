@@ -105,8 +105,30 @@ def _aligned_grad(g: torch.Tensor) -> torch.Tensor:
     return g if ok else _fresh(g)
 
 
+_DQ_SUM_MODES = ("auto", "split", "turns")
+_dq_sum = "auto"
+
+
+def set_dq_sum(mode: str) -> str:
+    """How the backward sums dQ over key blocks; returns the previous setting. Both ways are
+    deterministic (a fixed order per query tile):
+      "split": each key block writes its partials to the workspace (about 4 s^2 b h bytes) and a
+               third kernel sums them -- no workgroup waits on another;
+      "turns": key blocks add into dQ in place under turn counters (minimum workspace);
+      "auto" (default): "split" unless its workspace exceeds the library's FATTN_SPLIT_MAX_BYTES.
+    """
+    global _dq_sum
+    if mode not in _DQ_SUM_MODES:
+        raise ValueError(f"set_dq_sum: mode must be one of {_DQ_SUM_MODES}, got {mode!r}")
+    prev, _dq_sum = _dq_sum, mode
+    return prev
+
+
 def _workspace(b: int, h: int, s: int, device: torch.device) -> torch.Tensor:
-    nbytes = int(_lib.lib().fattn_bwd_workspace_bytes(b, h, s))
+    L = _lib.lib()
+    size = {"auto": L.fattn_bwd_workspace_bytes, "split": L.fattn_bwd_workspace_split_bytes,
+            "turns": L.fattn_bwd_workspace_min_bytes}[_dq_sum]
+    nbytes = int(size(b, h, s))
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 

@@ -19,10 +19,13 @@ Workspace workspace_layout(int64_t b, int64_t h, int64_t s) {
   Workspace w{};
   const size_t rows = static_cast<size_t>(b * h * s);
   const size_t tiles = static_cast<size_t>(b * h * ((s + kBwdQueryTile - 1) / kBwdQueryTile));
+  const size_t nkb = static_cast<size_t>((s + kBwdKeys - 1) / kBwdKeys);
   w.d_off = 0;
   w.turn_off = up(rows * sizeof(float));
   w.ctrl_off = w.turn_off + up(tiles * sizeof(int));
-  w.bytes = w.ctrl_off + up(64 * sizeof(int));
+  w.part_off = w.ctrl_off + up(64 * sizeof(int));
+  w.bytes_min = w.part_off;
+  w.bytes_split = w.part_off + up(nkb * tiles * kBwdQueryTile * kHeadDim * sizeof(float));
   return w;
 }
 
@@ -125,6 +128,7 @@ int run_forward(const char* who, View q, View k, View v, float* o, float* lse, i
 
 struct WsParts {
   float* dsum;
+  float* part;  // null: the workspace is too small for the split partials (turn hand-over)
   int* turn;
   int* ctrl;
 };
@@ -132,12 +136,14 @@ struct WsParts {
 int workspace_parts(const char* who, void* ws, size_t ws_bytes, int64_t b, int64_t h, int64_t s,
                     WsParts* out) {
   const fattn::Workspace l = fattn::workspace_layout(b, h, s);
-  if (!ws || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0 || ws_bytes < l.bytes) {
+  if (!ws || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0 || ws_bytes < l.bytes_min) {
     return fail(FATTN_EWORKSPACE, std::string(who) + ": the backward needs a 256-byte aligned " +
-                                      "workspace of " + std::to_string(l.bytes) + " bytes");
+                                      "workspace of at least " + std::to_string(l.bytes_min) +
+                                      " bytes");
   }
   char* base = static_cast<char*>(ws);
   out->dsum = reinterpret_cast<float*>(base + l.d_off);
+  out->part = ws_bytes >= l.bytes_split ? reinterpret_cast<float*>(base + l.part_off) : nullptr;
   out->turn = reinterpret_cast<int*>(base + l.turn_off);
   out->ctrl = reinterpret_cast<int*>(base + l.ctrl_off);
   return 0;
@@ -175,7 +181,7 @@ int run_bwd_main(const char* who, View q, View k, View v, View d_o, const float*
   }
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, &p)) return rc;
-  const int err = fattn::launch_bwd_main(q, k, v, d_o, lse, p.dsum, dqkv, p.turn, p.ctrl,
+  const int err = fattn::launch_bwd_main(q, k, v, d_o, lse, p.dsum, dqkv, p.part, p.turn, p.ctrl,
                                          static_cast<int>(b), static_cast<int>(h),
                                          static_cast<int>(s), scale, causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 2 launch");
@@ -258,7 +264,18 @@ const char* fattn_version(void) { return "fattn-gfx950 0.1.0 (head_dim 64, fp32 
 
 size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s) {
   if (b < 0 || h < 0 || s < 0) return 0;
-  return fattn::workspace_layout(b, h, s).bytes;
+  const fattn::Workspace l = fattn::workspace_layout(b, h, s);
+  return l.bytes_split <= FATTN_SPLIT_MAX_BYTES ? l.bytes_split : l.bytes_min;
+}
+
+size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s) {
+  if (b < 0 || h < 0 || s < 0) return 0;
+  return fattn::workspace_layout(b, h, s).bytes_min;
+}
+
+size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s) {
+  if (b < 0 || h < 0 || s < 0) return 0;
+  return fattn::workspace_layout(b, h, s).bytes_split;
 }
 
 int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,

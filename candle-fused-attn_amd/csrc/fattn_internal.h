@@ -26,11 +26,14 @@ struct View {
 };
 
 // Workspace of the backward, in this order, each part 256-byte aligned:
-//   D      [b, h, s] f32             rowsum(dO o O)
-//   turn   [b, h, ceil(s / 32)] i32  dQ turn counter per query tile
-//   ctrl   64 i32                    [0] key-block ticket, [32] guard word (spin bound hit)
+//   D      [b, h, s] f32                    rowsum(dO o O)
+//   turn   [b, h, ntile] i32                dQ turn counter per query tile (turn hand-over)
+//   ctrl   64 i32                           [0] key-block ticket, [32] guard word
+//   part   [nkb, b, h, ntile, kQT * 64] f32 dQ partial per key block and query tile (split only)
+// with ntile = ceil(s / kBwdQueryTile), nkb = ceil(s / kBwdKeys). `bytes_min` covers D, turn and
+// ctrl (the turn hand-over), `bytes_split` all four.
 struct Workspace {
-  size_t d_off, turn_off, ctrl_off, bytes;
+  size_t d_off, turn_off, ctrl_off, part_off, bytes_min, bytes_split;
 };
 Workspace workspace_layout(int64_t b, int64_t h, int64_t s);
 constexpr int kCtrlTicket = 0;
@@ -42,14 +45,16 @@ int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, i
                    float scale, int causal, void* stream);
 int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl, int b, int h,
                     int s, void* stream);
+// part == nullptr: the turn hand-over; else the split partials (and step 3, launched here too).
 int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
-                    float* dqkv, int* turn, int* ctrl, int b, int h, int s, float scale,
-                    int causal, void* stream);
+                    float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s,
+                    float scale, int causal, void* stream);
 
 // Grid sizes the launchers will use (for range checks before launching).
 int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal);
 int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s);
 int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s);
+int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s);
 
 }  // namespace fattn
 

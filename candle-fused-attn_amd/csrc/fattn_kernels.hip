@@ -21,9 +21,14 @@
 // L and D are [b, h, s]; dQ, dK, dV are written interleaved into one [b, s, 3, h, 64] buffer.
 //
 // Determinism: every sum has an order fixed by the shape alone. The cross-workgroup sum (dQ over
-// key blocks) is done in key-block order under one turn counter per (b, h, query tile); key blocks
-// are handed out by a ticket in arrival order, so a workgroup only ever waits on a key block that a
-// running workgroup already holds (no assumption about dispatch order).
+// key blocks) is done one of two ways, chosen by the size of the caller's workspace:
+//   split: every key block writes its dQ partial of each query tile to its own slot of the
+//     workspace (no workgroup waits on another); a second kernel sums the slots in key-block
+//     order, scales, and writes dQ;
+//   turns: key blocks add into dQ in place, in an order fixed per tile, under one turn counter per
+//     (b, h, query tile); key blocks are handed out by a ticket in arrival order, so a workgroup
+//     only ever waits on a key block that a running workgroup already holds (no assumption about
+//     dispatch order). Needs no workspace beyond D and the counters.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -351,26 +356,29 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward, step 2. One workgroup = one key block of 64 keys of one (b, h), taken by ticket;
-// wave w owns keys k0 + 16 w .. + 15, one per lane column lo, with K and V of its key in registers
-// (the B operands of S and dP), the block's K in the layout of the dQ product's B operand
-// (registers too), and dK^T, dV^T of its keys in accumulators. It walks query tiles of 32 (two
-// 16-query subtiles m; causal: from the block's first key on), the next tile's Q, dO, L, D in
-// flight during this one (LDS double buffer, filled by direct global -> LDS copies).
+// Backward, step 2. One workgroup = one key block of 64 keys of one (b, h) (split: by workgroup
+// index; turns: by ticket); wave w owns keys k0 + 16 w .. + 15, one per lane column lo, with K and
+// V of its key in registers (the B operands of S and dP), the block's K in the layout of the dQ
+// product's B operand (registers too), and dK^T, dV^T of its keys in accumulators. It walks query
+// tiles of kQT = 16 (kNS = 1 subtile m of 16 queries; causal: from the block's first key on), the
+// next tile's Q, dO, L, D in flight during this one (LDS double buffer, filled by direct global ->
+// LDS copies).
 //   S = Q K^T and dP = dO V^T per subtile: M = queries, N = the wave's keys, contraction over d;
 //   A = Q / dO [query 16 m + lo][dim 16 g + t] (LDS, float4 reads), B = K / V [key lo][16 g + t].
 //   P = exp(S scale - L), dS = P o (dP - D), in place in the accumulators.
-//   dV^T += dO^T P, dK^T += Q^T dS: M = dims, N = keys, contraction over the tile's 32 queries;
+//   dV^T += dO^T P, dK^T += Q^T dS: M = dims, N = keys, contraction over the tile's queries;
 //   step (m, r) uses query 16 m + 4 g + r: the P / dS value lane (lo, g) holds in register r of
 //   subtile m.
 //   dQ partial = dS K over the block's 64 keys: dS goes through LDS (the one product that needs
 //   queries in lo); wave w computes dims 16 w .. + 15, step t contracting keys 16 g + t:
 //   A = dS[16 m + lo][16 g + t] (LDS, float4 reads), B = K[k0 + 16 g + t][16 w + lo] (registers).
-// The partial is added into dQ on the tile's turn, one tile later (software pipelined: while tile
-// t + 1's products run, the loads of what the earlier key blocks summed for tile t are in
-// flight): key block 0 stores, the others add their partial to what they read, the last
-// contributor scales; then the turn passes to the next key block. The tile's dQ is therefore
-// ((p0 + p1) + p2) + ... in key-block order on every run.
+// split: the partial is stored to the key block's slot at the start of the next tile (plain
+// stores, nothing waits for them); step 3 (dq_kernel) sums the slots.
+// turns: the partial is added into dQ on the tile's turn, one tile later (software pipelined:
+// while tile t + 1's products run, the loads of what the earlier key blocks summed for tile t are
+// in flight): the first contributor stores, the others add their partial to what they read, the
+// last contributor scales; then the turn passes to the next key block.
+// Either way a tile's dQ is ((p_0 + p_1) + p_2) + ... in a fixed key-block order, times scale.
 // ---------------------------------------------------------------------------------------------
 #ifndef BWD_WAVES
 #define BWD_WAVES 3
@@ -385,6 +393,7 @@ struct BwdArgs {
   const float* lse;
   const float* dsum;
   float* dqkv;
+  float* part;  // split: the dQ partials, [nkb][b h][ntile][kQT * 64] in fragment order
   int* turn;
   int* ctrl;
   int B, H, S, nkb, ntile;
@@ -422,6 +431,11 @@ static_assert(kStage1Loads == 4, "wait_except_stage1 encodes vmcnt(4)");
 __device__ __forceinline__ void wait_except_stage1() {
   asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
 }
+// split: everything but the partial's kNS stores, issued after the next tile's copies.
+static_assert(kNS == 1, "wait_except_part encodes vmcnt(1)");
+__device__ __forceinline__ void wait_except_part() {
+  asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+}
 
 // Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised.
 __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
@@ -441,6 +455,7 @@ __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
 
 // Occupancy target: BWD_WAVES waves per SIMD (the kernel is latency-bound: with fewer, the
 // matrix cores idle behind barriers and the dQ hand-over).
+template <bool kSplit>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BWD_WAVES)))
 bwd_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) float sQ[2][kQT * kHeadDim];
@@ -450,21 +465,33 @@ bwd_kernel(BwdArgs a) {
   __shared__ int s_item;
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lo = lane & 15, g = lane >> 4;
-  // Ticket: the key block this workgroup computes, in arrival order. Key block kb of a (b, h) has a
-  // later item than kb - 1, so the block it waits on was taken by an earlier, running workgroup.
-  if (tid == 0) s_item = atomicAdd(a.ctrl + kCtrlTicket, 1);
-  __syncthreads();
-  const int item = s_item;
-  if (item >= a.nkb * a.B * a.H) {
-    // The ticket was not cleared by step 1 on this workspace: refuse (no access out of range),
-    // and raise the guard word so the caller can tell.
-    if (tid == 0) __hip_atomic_store(a.ctrl + kCtrlGuard, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
+  const int BH = a.B * a.H;
+  int item;
+  if (kSplit) {
+    // No workgroup waits on another: the workgroup index is the item. Non-causal: the key blocks
+    // of one (b, h) on one XCD (they read the same Q and dO tiles at about the same time).
+    // Causal: round-robin over the XCDs, which spreads the expensive low blocks evenly.
+    const int n = static_cast<int>(gridDim.x), id = static_cast<int>(blockIdx.x);
+    item = a.causal ? id : xcd_remap(id, n);
+  } else {
+    // Ticket: the key block this workgroup computes, in arrival order. Key block kb of a (b, h)
+    // has a later item than kb - 1, so the block it waits on was taken by an earlier, running
+    // workgroup.
+    if (tid == 0) s_item = atomicAdd(a.ctrl + kCtrlTicket, 1);
+    __syncthreads();
+    item = s_item;
+    if (item >= a.nkb * BH) {
+      // The ticket was not cleared by step 1 on this workspace: refuse (no access out of range),
+      // and raise the guard word so the caller can tell.
+      if (tid == 0) {
+        __hip_atomic_store(a.ctrl + kCtrlGuard, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return;
+    }
   }
   // Non-causal: (b, h)-major, the key blocks of one (b, h) adjacent. Causal: key-block-major, so
   // the expensive low blocks (they see every later query) start first. Either way key block kb
   // of a (b, h) comes after kb - 1.
-  const int BH = a.B * a.H;
   const int bh = a.causal ? item % BH : item / a.nkb;
   const int kb = a.causal ? item / BH : item % a.nkb;
   const int b = bh / a.H, h = bh % a.H, S = a.S;
@@ -627,6 +654,15 @@ bwd_kernel(BwdArgs a) {
       }
     }
   };
+  // split: this block's partial of the tile at q0p into its slot, in fragment order (register r
+  // of lane l of wave w, subtile m at m kQT 16 + w 256 + 4 l + r: one contiguous 1 KB store per
+  // wave and subtile).
+  auto store_part = [&](int q0p, const f4 (&part)[kNS]) {
+    float* dst = a.part + ((static_cast<int64_t>(kb) * BH + bh) * a.ntile + q0p / kQT) *
+                              (kQT * kHeadDim) + 256 * w + 4 * lane;
+#pragma unroll
+    for (int m = 0; m < kNS; ++m) st4(dst + m * (16 * kHeadDim), part[m]);
+  };
   // After stage 2's stores completed (vmcnt(0) and a barrier): the next contributor's turn.
   auto pass_turn = [&](int q0p, int pos, int cnt) {
     if (pos + 1 < cnt && tid == 0) {
@@ -647,13 +683,17 @@ bwd_kernel(BwdArgs a) {
     if (has_next) gload(tile_at(t + 1) * kQT, sQ[buf ^ 1], sdO[buf ^ 1]);
     const float* Qt = sQ[buf];
     const float* Gt = sdO[buf];
-    // Stage 1's turn, read early (one lane, no wait here): by the time it is checked below the
-    // value has arrived, and usually the turn with it.
     int seen = -1;
-    if (p1_q0 >= 0 && p1_pos > 0 && lane == 0) {
-      seen = __hip_atomic_load(tp + p1_q0 / kQT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (kSplit) {
+      if (p1_q0 >= 0) store_part(p1_q0, p1);  // the last tile's partial
+    } else {
+      // Stage 1's turn, read early (one lane, no wait here): by the time it is checked below the
+      // value has arrived, and usually the turn with it.
+      if (p1_q0 >= 0 && p1_pos > 0 && lane == 0) {
+        seen = __hip_atomic_load(tp + p1_q0 / kQT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (p2_q0 >= 0) store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);  // stage 2, two tiles back
     }
-    if (p2_q0 >= 0) store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);  // stage 2, two tiles back
     compiler_fence();
 
     // Wave-uniform liveness of each 16-query subtile for this wave's 16 keys.
@@ -686,7 +726,7 @@ bwd_kernel(BwdArgs a) {
       }
     }
 
-    if (p1_q0 >= 0) load_sums(p1_q0, p1_pos, seen, p1s);  // stage 1, one tile back
+    if (!kSplit && p1_q0 >= 0) load_sums(p1_q0, p1_pos, seen, p1s);  // stage 1, one tile back
 
     // P = exp(S scale - L), dS = P o (dP - D); lane (lo, g), register r of subtile m: query
     // q0 + 16 m + 4 g + r, key `key`. Then dV^T and dK^T.
@@ -718,25 +758,35 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) sdS[(16 * m + 4 * g + r) * kBwdLd + 16 * w + lo] = sP[m][r];
     }
-    // Stage 2's stores and the next tile's copies complete (stage 1's loads, issued last, may
-    // still be in flight: they are needed only in the next iteration).
-    if (p1_q0 >= 0 && p1_pos > 0) {
-      wait_except_stage1();
+    if (kSplit) {
+      // The next tile's copies complete (the partial's stores, issued after them, need not).
+      if (p1_q0 >= 0) {
+        wait_except_part();
+      } else {
+        wait_mem();
+      }
+      __syncthreads();  // dS complete
     } else {
-      wait_mem();
-    }
-    __syncthreads();  // dS complete; every wave's stage-2 stores complete
-    if (p2_q0 >= 0) pass_turn(p2_q0, p2_pos, p2_cnt);
+      // Stage 2's stores and the next tile's copies complete (stage 1's loads, issued last, may
+      // still be in flight: they are needed only in the next iteration).
+      if (p1_q0 >= 0 && p1_pos > 0) {
+        wait_except_stage1();
+      } else {
+        wait_mem();
+      }
+      __syncthreads();  // dS complete; every wave's stage-2 stores complete
+      if (p2_q0 >= 0) pass_turn(p2_q0, p2_pos, p2_cnt);
 
-    // Stages advance; this tile's dQ partial enters stage 1.
-    p2_q0 = p1_q0;
-    p2_pos = p1_pos;
-    p2_cnt = p1_cnt;
+      // Stages advance; this tile's dQ partial enters stage 1.
+      p2_q0 = p1_q0;
+      p2_pos = p1_pos;
+      p2_cnt = p1_cnt;
 #pragma unroll
-    for (int m = 0; m < kNS; ++m) {
-      p2[m] = p1[m];
+      for (int m = 0; m < kNS; ++m) {
+        p2[m] = p1[m];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) p2s[m][r] = p1s[m][r];
+        for (int r = 0; r < 4; ++r) p2s[m][r] = p1s[m][r];
+      }
     }
 #pragma unroll
     for (int m = 0; m < kNS; ++m) {
@@ -759,14 +809,16 @@ bwd_kernel(BwdArgs a) {
     __syncthreads();  // dS read by every wave; the next tile's L and D staged
   }
 
-  // Drain: the two tiles still in the pipeline, in order.
-  if (p2_q0 >= 0) {
+  // Drain: the tiles still in the pipeline, in order.
+  if (kSplit) {
+    if (p1_q0 >= 0) store_part(p1_q0, p1);
+  } else if (p2_q0 >= 0) {
     store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);
     wait_stores();
     __syncthreads();
     pass_turn(p2_q0, p2_pos, p2_cnt);
   }
-  if (p1_q0 >= 0) {
+  if (!kSplit && p1_q0 >= 0) {
     load_sums(p1_q0, p1_pos, -1, p1s);
     store_sums(p1_q0, p1_pos, p1_cnt, p1, p1s);
     wait_stores();
@@ -787,6 +839,42 @@ bwd_kernel(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Backward, step 3 (split only): dQ of one (b, h, query tile) per workgroup, the tile's partials
+// summed in key-block order, ((p_0 + p_1) + p_2) + ..., times scale (the same operations, in the
+// same order, as the turn hand-over). Thread i reads float4 i of each partial (fragment order:
+// lane l of wave w, registers r = 0..3 -> query 4 (l / 16) + r, dim 16 w + l % 16), then the tile
+// goes through LDS so that every row of dQ is written as 16 float4s.
+// ---------------------------------------------------------------------------------------------
+static_assert(kQT * kHeadDim == 4 * kThreads, "dq_kernel: one float4 of the tile per thread");
+
+__global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ part,
+                                                     float* __restrict__ dqkv, int B, int H,
+                                                     int S, int nkb, int ntile, float scale,
+                                                     int causal) {
+  __shared__ __attribute__((aligned(16))) float tile[kQT * kBwdLd];
+  const int tid = threadIdx.x;
+  const int bh = static_cast<int>(blockIdx.x) / ntile, j = static_cast<int>(blockIdx.x) % ntile;
+  const int b = bh / H, h = bh % H, q0 = j * kQT;
+  // Contributors: causal, the key blocks holding a key <= the tile's last query.
+  const int cnt = causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) + 1 : nkb;
+  const int64_t slot = static_cast<int64_t>(B) * H * ntile * (kQT * kHeadDim);
+  const float* src = part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * kHeadDim) + 4 * tid;
+  f4 acc = ld4(src);
+  for (int kb = 1; kb < cnt; ++kb) acc += ld4(src + kb * slot);
+  acc *= scale;
+  const int w = tid >> 6, lane = tid & 63, lo = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) tile[(4 * g + r) * kBwdLd + 16 * w + lo] = acc[r];
+  __syncthreads();
+  const int row = tid >> 4, c4 = tid & 15;
+  if (q0 + row < S) {
+    st4(dqkv + (static_cast<int64_t>(b) * S + q0 + row) * 3 * H * kHeadDim +
+            static_cast<int64_t>(h) * kHeadDim + 4 * c4,
+        ld4(&tile[row * kBwdLd + 4 * c4]));
+  }
+}
+
 }  // namespace
 
 // The two forward shapes: queries per workgroup, keys per tile.
@@ -801,6 +889,7 @@ int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s) {
   return ((s + kBwdKeys - 1) / kBwdKeys) * h * b;
 }
 int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s) { return (b * h * s + 15) / 16; }
+int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQT - 1) / kQT); }
 
 int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s,
                    float scale, int causal, void* stream) {
@@ -826,16 +915,26 @@ int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl,
 }
 
 int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
-                    float* dqkv, int* turn, int* ctrl, int b, int h, int s, float scale,
-                    int causal, void* stream) {
-  const int nkb = (s + kBwdKeys - 1) / kBwdKeys;
-  BwdArgs a{q, k, v, d_o, lse, dsum, dqkv, turn, ctrl, b, h, s,
-            nkb, (s + kQT - 1) / kQT, scale, causal, !causal && nkb <= kStaggerMaxBlocks ? 1 : 0};
+                    float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s,
+                    float scale, int causal, void* stream) {
+  int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
+  const bool split = part != nullptr;
+  const int stagger = !split && !causal && nkb <= kStaggerMaxBlocks ? 1 : 0;
+  BwdArgs a{q, k, v, d_o, lse, dsum, dqkv, part, turn, ctrl, b, h, s,
+            nkb, ntile, scale, causal, stagger};
   void* args[] = {&a};
-  return static_cast<int>(hipLaunchKernel(reinterpret_cast<const void*>(bwd_kernel),
-                                          dim3(static_cast<unsigned>(bwd_main_blocks(b, h, s))),
-                                          dim3(kThreads), args, 0,
-                                          static_cast<hipStream_t>(stream)));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const void* fn = split ? reinterpret_cast<const void*>(bwd_kernel<true>)
+                         : reinterpret_cast<const void*>(bwd_kernel<false>);
+  hipError_t err = hipLaunchKernel(fn, dim3(static_cast<unsigned>(bwd_main_blocks(b, h, s))),
+                                   dim3(kThreads), args, 0, st);
+  if (err != hipSuccess || !split) return static_cast<int>(err);
+  const float* cpart = part;
+  void* args3[] = {&cpart, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
+  err = hipLaunchKernel(reinterpret_cast<const void*>(dq_kernel),
+                        dim3(static_cast<unsigned>(bwd_dq_blocks(b, h, s))), dim3(kThreads),
+                        args3, 0, st);
+  return static_cast<int>(err);
 }
 
 }  // namespace fattn

@@ -60,10 +60,19 @@ int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, 
                       const int64_t q_strides[3], const int64_t k_strides[3],
                       const int64_t v_strides[3], void* stream);
 
-/* Bytes of device workspace the backward needs: D = rowsum(dO o O) [b, h, s] f32, the dQ turn
- * counters and the key-block ticket. Replaces the temporaries cuda::backward allocates
- * (dsum and turn, src/cuda.rs:200-209). Workspace must be 256-byte aligned. */
+/* Backward workspace (256-byte aligned). Replaces the temporaries cuda::backward allocates
+ * (dsum and turn, src/cuda.rs:200-209). Its size picks how dQ is summed over key blocks:
+ *   >= fattn_bwd_workspace_split_bytes: "split" -- every key block writes its dQ partials to the
+ *      workspace (about 4 * s * s * b * h bytes) and a third kernel sums them in key-block order;
+ *      no workgroup waits on another (the faster way);
+ *   >= fattn_bwd_workspace_min_bytes (below split): "turns" -- key blocks add into dQ in place,
+ *      in key-block order, under per-query-tile turn counters; D, counters and ticket only.
+ * Both are deterministic. fattn_bwd_workspace_bytes is the split size when that is at most
+ * FATTN_SPLIT_MAX_BYTES, else the minimum. */
+#define FATTN_SPLIT_MAX_BYTES ((size_t)4 << 30)
 size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s);
+size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s);
+size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s);
 
 /* Backward step 1: D[b, h, i] = sum_c dO[b, i, h, c] * O[b, i, h, c] (fixed order) and the
  * counters of step 2 cleared. O is [b, s, h, 64] contiguous; dO is read through do_strides.
@@ -73,9 +82,9 @@ int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_st
                            int64_t b, int64_t h, int64_t s, int64_t d, void* stream);
 
 /* Backward step 2: dK, dV and dQ into ONE [b, s, 3, h, 64] buffer (the fused qkv projection's
- * gradient layout), dQ added in key-block order under per-query-tile turn counters, so every
- * rerun is bit-identical. Needs step 1 on the same workspace first. Replaces the
- * fattn_bwd_f32_d64 launch (src/cuda.rs:233-258). */
+ * gradient layout); dQ summed over key blocks in a fixed order (split or turns, by workspace
+ * size, see above), so every rerun is bit-identical. Needs step 1 on the same workspace first.
+ * Replaces the fattn_bwd_f32_d64 launch (src/cuda.rs:233-258). */
 int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
                            const float* lse, float* dqkv, void* workspace,
                            size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,

@@ -47,11 +47,19 @@ def a3(*x):
 def test_workspace_size_is_aligned_and_monotone():
     L = _lib.lib()
     n1 = L.fattn_bwd_workspace_bytes(64, 6, 240)
-    assert n1 % 256 == 0
-    # D (64*6*240 f32) + turns (64*6*15 i32) + control
-    assert n1 >= 64 * 6 * 240 * 4 + 64 * 6 * 15 * 4 + 256
+    lo, hi = L.fattn_bwd_workspace_min_bytes(64, 6, 240), L.fattn_bwd_workspace_split_bytes(64, 6, 240)
+    assert n1 % 256 == 0 and lo % 256 == 0 and hi % 256 == 0
+    # minimum: D (64*6*240 f32) + turns (64*6*15 i32) + control
+    assert lo >= 64 * 6 * 240 * 4 + 64 * 6 * 15 * 4 + 256
+    # split: plus one 16 x 64 f32 partial per key block (4) and query tile (15) of each (b, h)
+    assert hi == lo + 4 * 64 * 6 * 15 * 16 * 64 * 4
+    assert n1 == hi  # 94 MB: below the split cap
     assert L.fattn_bwd_workspace_bytes(64, 6, 241) >= n1
     assert L.fattn_bwd_workspace_bytes(-1, 6, 240) == 0
+    assert L.fattn_bwd_workspace_min_bytes(-1, 6, 240) == 0
+    # Past FATTN_SPLIT_MAX_BYTES (4 GiB) the default falls back to the minimum (turns).
+    assert L.fattn_bwd_workspace_split_bytes(1, 64, 16384) > 4 << 30
+    assert L.fattn_bwd_workspace_bytes(1, 64, 16384) == L.fattn_bwd_workspace_min_bytes(1, 64, 16384)
 
 
 def test_head_dim_gate_before_alignment():

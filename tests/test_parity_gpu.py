@@ -38,6 +38,14 @@ def say(*a):
     print(*a, flush=True)
 
 
+@pytest.fixture(params=["split", "turns"])
+def dq_sum(request):
+    """Runs a test under each way of summing dQ over key blocks (the workspace size picks it)."""
+    prev = cfa.set_dq_sum(request.param)
+    yield request.param
+    cfa.set_dq_sum(prev)
+
+
 # --- the reference test's harness (tests/parity.rs:28-123) --------------------------------
 
 def qkv_views(qkv, h, d):
@@ -190,11 +198,11 @@ def test_entry_points_agree(orc, cuda, causal):
 
 @pytest.mark.parametrize("path", ["fused", "fused_qkv"])
 @pytest.mark.parametrize("causal", [False, True])
-def test_backward_is_deterministic(orc, cuda, causal, path):
-    """dQ is summed over key blocks under turn counters: reruns are bit-identical
+def test_backward_is_deterministic(orc, cuda, causal, path, dq_sum):
+    """dQ is summed over key blocks in a fixed order: reruns are bit-identical
     (tests/parity.rs:223-242, 8 reruns)."""
     b, s, h, d = 4, 240, 6, 64
-    say(f"determinism {path} causal={causal}")
+    say(f"determinism {path} causal={causal} {dq_sum}")
     x, w = orc.closed_form_inputs(b, s, h, d)
     qkv, wt = torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda)
     o1, g1 = run(path, qkv, wt, h, d, causal)
@@ -208,13 +216,13 @@ def test_backward_is_deterministic(orc, cuda, causal, path):
 # --- edge cases ------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_sequence_lengths(orc, cuda, causal):
+def test_sequence_lengths(orc, cuda, causal, dq_sum):
     """Tails of every kind: single key, partial 16-query tiles, partial 64-key blocks."""
     rng = np.random.default_rng(3)
     for s in (1, 2, 15, 16, 17, 48, 63, 64, 65, 100, 129, 200):
         x = rng.standard_normal((2, s, 3 * 2 * 64)).astype(np.float32)
         w = rng.standard_normal((2, s, 2 * 64)).astype(np.float32)
-        say(f"seq {s} causal={causal}")
+        say(f"seq {s} causal={causal} {dq_sum}")
         ref_out, _, ref_grad = oracle_qkv(orc, x, w, 2, 64, causal, np.float64, 0.125)
         out, grad = run("fused_qkv", torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda),
                         2, 64, causal, 0.125)
@@ -325,8 +333,9 @@ def test_config2_target(orc, cuda):
     check_errors(orc, out, grad, ref_out, ref_grad, "config2")
 
 
-def test_config3_causal_reruns(orc, cuda):
+def test_config3_causal_reruns(orc, cuda, dq_sum):
     """Config 2's shape, causal, plus 10 backward reruns compared bitwise."""
+    say(f"config3 {dq_sum}")
     x, dout, qkv, g = seeded_qkv(orc, 64, 6, 240, 0, cuda)
     ref_out, _, ref_grad = oracle_qkv(orc, x, dout, 6, 64, True, np.float64, 0.125)
     out, grad = run("fused_qkv", qkv, g, 6, 64, True, 0.125)
@@ -416,16 +425,45 @@ def test_config5_strided_views_large_logits(orc, cuda):
 
 
 @pytest.mark.parametrize("s", [4096, 4160])
-def test_long_sequences_both_walk_orders(orc, cuda, s):
-    """Non-causal key blocks walk staggered over the tiles up to 64 blocks per (b, h) (s 4096)
-    and in index order beyond (s 4160): both against fp64, and bit-identical reruns."""
+def test_long_sequences_both_walk_orders(orc, cuda, s, dq_sum):
+    """Turns: non-causal key blocks walk staggered over the tiles up to 64 blocks per (b, h)
+    (s 4096) and in index order beyond (s 4160); split: index order. Against fp64, and
+    bit-identical reruns."""
     rng = np.random.default_rng(s)
     x = rng.standard_normal((1, s, 3 * 64)).astype(np.float32)
     w = rng.standard_normal((1, s, 64)).astype(np.float32)
-    say(f"long non-causal s{s}")
+    say(f"long non-causal s{s} {dq_sum}")
     ref_out, _, ref_grad = oracle_qkv(orc, x, w, 1, 64, False, np.float64, 0.125)
     qkv, wt = torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda)
     out, grad = run("fused_qkv", qkv, wt, 1, 64, False, 0.125)
     check_errors(orc, out, grad, ref_out, ref_grad, f"s{s}")
     _, grad2 = run("fused_qkv", qkv, wt, 1, 64, False, 0.125)
     assert torch.equal(bits(grad), bits(grad2))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_split_and_turns_agree(orc, cuda, causal):
+    """The two ways of summing dQ. Causal: both walk each key block's tiles upward and sum dQ in
+    key-block order, so O and the whole gradient are bit-identical. Non-causal: turns walk the
+    tiles from a staggered start (so dK and dV accumulate in another order) and sum dQ in that
+    order: O is identical, the gradient agrees to rounding."""
+    b, h, s = 8, 6, 240
+    x, dout, qkv, g = seeded_qkv(orc, b, h, s, 0, cuda)
+    res = {}
+    for mode in ("split", "turns"):
+        say(f"agree causal={causal} {mode}")
+        prev = cfa.set_dq_sum(mode)
+        try:
+            res[mode] = run("fused_qkv", qkv, g, h, 64, causal, 0.125)
+        finally:
+            cfa.set_dq_sum(prev)
+    (o1, g1), (o2, g2) = res["split"], res["turns"]
+    assert torch.equal(bits(o1), bits(o2))
+    if causal:
+        assert torch.equal(bits(g1), bits(g2))
+    else:
+        for i, name in enumerate(("dQ", "dK", "dV")):
+            a, b_ = g1[..., i * h * 64:(i + 1) * h * 64], g2[..., i * h * 64:(i + 1) * h * 64]
+            rel = ((a - b_).norm() / b_.norm()).item()
+            say(f"  {name} split vs turns: {rel:.2e}")
+            assert rel <= 1e-6
