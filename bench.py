@@ -116,6 +116,11 @@ def main() -> int:
                                             ws_bytes, B, H, S, D, SCALE, ci, qst, qst, qst, gst,
                                             sp))
 
+    def dq_k():
+        _lib.check(L.fattn_bwd_dq_f32_d64(P(dqkv), P(ws), ws_bytes, B, H, S, D, SCALE, ci, sp))
+
+    split = ws_bytes >= int(L.fattn_bwd_workspace_split_bytes(B, H, S))
+
     if args.calibrate_copy:
         src = torch.ones(64 * 1024 * 1024, device=dev)   # 256 MiB
         dst = torch.empty_like(src)
@@ -148,25 +153,29 @@ def main() -> int:
     fwd_ms, _ = timed(fwd, K)
     log(f"bench: fwd+bwd {fwd_bwd_ms:.4f} ms (wall {fwd_bwd_wall:.4f}), fwd {fwd_ms:.4f} ms")
 
-    # Per-kernel durations from HIP events on the launch stream, one launch per bracket.
-    def per_kernel(fn, before=None, n=K):
-        ts = []
-        for _ in range(n):
-            if before:
-                before()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
+    # Per-kernel durations: K more steps, back to back as above, with the backward launched as
+    # its kernel-level steps (the same kernels on the same arguments as fattn_qkv_backward) and a
+    # HIP event on the launch stream between every two launches.
+    kernels = [("fwd", fwd), ("bwd_prep", prep_k), ("bwd_main", main_k)]
+    if split:
+        kernels.append(("bwd_dq", dq_k))
+    marks = []
+    torch.cuda.synchronize()
+    for _ in range(K):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)]
+        ev[0].record(stream)
+        for i, (_, fn) in enumerate(kernels):
             fn()
-            e1.record(stream)
-            ts.append((e0, e1))
-        torch.cuda.synchronize()
-        return statistics.mean(a.elapsed_time(b) for a, b in ts) * 1e3  # us
-
-    fwd()
-    fwd_us = per_kernel(fwd)
-    prep_us = per_kernel(prep_k)
-    main_us = per_kernel(main_k, before=prep_k)
-    log(f"bench: kernels fwd {fwd_us:.1f} us, prep {prep_us:.1f} us, bwd main {main_us:.1f} us")
+            ev[i + 1].record(stream)
+        marks.append(ev)
+    torch.cuda.synchronize()
+    kus = {name: statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in marks) * 1e3
+           for i, (name, _) in enumerate(kernels)}
+    steps_us = statistics.mean(ev[0].elapsed_time(ev[-1]) for ev in marks) * 1e3
+    fwd_us, prep_us, main_us = kus["fwd"], kus["bwd_prep"], kus["bwd_main"]
+    dq_us = kus.get("bwd_dq", 0.0)
+    log(f"bench: kernels fwd {fwd_us:.1f} us, prep {prep_us:.1f} us, bwd main {main_us:.1f} us, "
+        f"dq sum {dq_us:.1f} us ({'split' if split else 'turns'}); step {steps_us:.1f} us")
 
     f_fwd, f_bwd = flops(B, H, S, D, causal)
     fwd_tflops = f_fwd / (fwd_ms * 1e-3) / 1e12
@@ -209,9 +218,12 @@ def main() -> int:
         "fwd_bwd_tflops": round(total_tflops, 3),
         "frac_fp32_peak": round(total_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
         "kernels_us": {"fwd": round(fwd_us, 2), "bwd_prep": round(prep_us, 2),
-                       "bwd_main": round(main_us, 2)},
+                       "bwd_main": round(main_us, 2), "bwd_dq": round(dq_us, 2),
+                       "step": round(steps_us, 2)},
+        "dq_sum": "split" if split else "turns",
         "roofline": {
-            "kernel": "bwd_kernel (fattn_bwd_main_f32_d64)",
+            "kernel": ("bwd_kernel<true> (fattn_bwd_main_f32_d64, split)" if split
+                       else "bwd_kernel<false> (fattn_bwd_main_f32_d64, turns)"),
             "bound": "mfma",
             "achieved": round(main_tflops, 3),
             "peak": PEAK_FP32_MFMA_TFLOPS,

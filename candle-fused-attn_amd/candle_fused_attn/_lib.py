@@ -27,6 +27,7 @@ EXPORTS = (
     "fattn_bwd_workspace_split_bytes",
     "fattn_bwd_prep_f32_d64",
     "fattn_bwd_main_f32_d64",
+    "fattn_bwd_dq_f32_d64",
     "fattn_bwd_f32_d64",
     "fattn_qkv_forward",
     "fattn_qkv_backward",
@@ -71,6 +72,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.fattn_bwd_prep_f32_d64.argtypes = [P, P, A3, P, SIZE, I64, I64, I64, I64, P]
     L.fattn_bwd_main_f32_d64.argtypes = [P, P, P, P, P, P, P, SIZE, I64, I64, I64, I64, C_FLOAT,
                                          C_INT, A3, A3, A3, A3, P]
+    L.fattn_bwd_dq_f32_d64.argtypes = [P, P, SIZE, I64, I64, I64, I64, C_FLOAT, C_INT, P]
     L.fattn_bwd_f32_d64.argtypes = [P, P, P, P, P, P, P, P, SIZE, I64, I64, I64, I64, C_FLOAT,
                                     C_INT, A3, A3, A3, A3, P]
     L.fattn_qkv_forward.argtypes = [P, I64, A3, A3, I64, C_FLOAT, C_INT, P, P, P]

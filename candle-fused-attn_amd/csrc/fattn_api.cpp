@@ -188,12 +188,33 @@ int run_bwd_main(const char* who, View q, View k, View v, View d_o, const float*
   return ok();
 }
 
+// Step 3: in split mode (the workspace holds the partials) dQ from the partials; else nothing.
+int run_bwd_dq(const char* who, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
+               int64_t s, float scale, int causal, void* stream) {
+  if (int rc = check_range(who, b, h, s)) return rc;
+  if (s * 3 * h * fattn::kHeadDim > int64_t{UINT32_MAX}) return slice_error(who, s);
+  if (!dqkv) return fail(FATTN_EINVAL, std::string(who) + ": null operand");
+  if (!aligned16(dqkv)) {
+    return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
+  }
+  WsParts p{};
+  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, &p)) return rc;
+  if (!p.part) return ok();
+  const int err = fattn::launch_bwd_dq(p.part, dqkv, static_cast<int>(b), static_cast<int>(h),
+                                       static_cast<int>(s), scale, causal ? 1 : 0, stream);
+  if (err) return hip_fail(err, "backward step 3 launch");
+  return ok();
+}
+
 int run_backward(const char* who, View q, View k, View v, const float* o, View d_o,
                  const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
                  int64_t s, float scale, int causal, void* stream) {
   if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, stream)) return rc;
-  return run_bwd_main(who, q, k, v, d_o, lse, dqkv, ws, ws_bytes, b, h, s, scale, causal,
-                      stream);
+  if (int rc = run_bwd_main(who, q, k, v, d_o, lse, dqkv, ws, ws_bytes, b, h, s, scale, causal,
+                            stream)) {
+    return rc;
+  }
+  return run_bwd_dq(who, dqkv, ws, ws_bytes, b, h, s, scale, causal, stream);
 }
 
 bool negative(const int64_t* x, int n) {
@@ -318,6 +339,15 @@ int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const
   return run_bwd_main("fused_attention", make_view(q, q_strides), make_view(k, k_strides),
                       make_view(v, v_strides), make_view(d_o, do_strides), lse, dqkv, workspace,
                       workspace_bytes, b, h, s, scale, causal, stream);
+}
+
+int fattn_bwd_dq_f32_d64(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b,
+                         int64_t h, int64_t s, int64_t d, float scale, int causal, void* stream) {
+  if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
+  if (int rc = check_head_dim(d)) return rc;
+  if (empty3(b, h, s)) return ok();
+  return run_bwd_dq("fused_attention", dqkv, workspace, workspace_bytes, b, h, s, scale, causal,
+                    stream);
 }
 
 int fattn_bwd_f32_d64(const float* q, const float* k, const float* v, const float* o,

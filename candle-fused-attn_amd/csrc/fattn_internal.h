@@ -45,10 +45,13 @@ int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, i
                    float scale, int causal, void* stream);
 int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl, int b, int h,
                     int s, void* stream);
-// part == nullptr: the turn hand-over; else the split partials (and step 3, launched here too).
+// part == nullptr: the turn hand-over (dQ final after step 2); else the split partials, which
+// step 3 (launch_bwd_dq) sums into dQ.
 int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
                     float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s,
                     float scale, int causal, void* stream);
+int launch_bwd_dq(const float* part, float* dqkv, int b, int h, int s, float scale, int causal,
+                  void* stream);
 
 // Grid sizes the launchers will use (for range checks before launching).
 int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal);

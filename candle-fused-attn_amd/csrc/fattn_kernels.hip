@@ -923,18 +923,22 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const fl
   BwdArgs a{q, k, v, d_o, lse, dsum, dqkv, part, turn, ctrl, b, h, s,
             nkb, ntile, scale, causal, stagger};
   void* args[] = {&a};
-  const hipStream_t st = static_cast<hipStream_t>(stream);
   const void* fn = split ? reinterpret_cast<const void*>(bwd_kernel<true>)
                          : reinterpret_cast<const void*>(bwd_kernel<false>);
-  hipError_t err = hipLaunchKernel(fn, dim3(static_cast<unsigned>(bwd_main_blocks(b, h, s))),
-                                   dim3(kThreads), args, 0, st);
-  if (err != hipSuccess || !split) return static_cast<int>(err);
-  const float* cpart = part;
-  void* args3[] = {&cpart, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
-  err = hipLaunchKernel(reinterpret_cast<const void*>(dq_kernel),
-                        dim3(static_cast<unsigned>(bwd_dq_blocks(b, h, s))), dim3(kThreads),
-                        args3, 0, st);
-  return static_cast<int>(err);
+  return static_cast<int>(hipLaunchKernel(fn,
+                                          dim3(static_cast<unsigned>(bwd_main_blocks(b, h, s))),
+                                          dim3(kThreads), args, 0,
+                                          static_cast<hipStream_t>(stream)));
+}
+
+int launch_bwd_dq(const float* part, float* dqkv, int b, int h, int s, float scale, int causal,
+                  void* stream) {
+  int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
+  void* args[] = {&part, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
+  return static_cast<int>(hipLaunchKernel(reinterpret_cast<const void*>(dq_kernel),
+                                          dim3(static_cast<unsigned>(bwd_dq_blocks(b, h, s))),
+                                          dim3(kThreads), args, 0,
+                                          static_cast<hipStream_t>(stream)));
 }
 
 }  // namespace fattn

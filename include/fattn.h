@@ -81,10 +81,11 @@ int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_st
                            void* workspace, size_t workspace_bytes,
                            int64_t b, int64_t h, int64_t s, int64_t d, void* stream);
 
-/* Backward step 2: dK, dV and dQ into ONE [b, s, 3, h, 64] buffer (the fused qkv projection's
- * gradient layout); dQ summed over key blocks in a fixed order (split or turns, by workspace
- * size, see above), so every rerun is bit-identical. Needs step 1 on the same workspace first.
- * Replaces the fattn_bwd_f32_d64 launch (src/cuda.rs:233-258). */
+/* Backward step 2: dK and dV into ONE [b, s, 3, h, 64] buffer (the fused qkv projection's
+ * gradient layout); dQ summed over key blocks in a fixed order, so every rerun is bit-identical:
+ * with a split-size workspace its partials go to the workspace (step 3 finishes dQ), else dQ is
+ * complete after this step. Needs step 1 on the same workspace first. Replaces the
+ * fattn_bwd_f32_d64 launch (src/cuda.rs:233-258). */
 int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
                            const float* lse, float* dqkv, void* workspace,
                            size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
@@ -92,7 +93,13 @@ int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const
                            const int64_t k_strides[3], const int64_t v_strides[3],
                            const int64_t do_strides[3], void* stream);
 
-/* Both backward steps. Replaces cuda::backward (src/cuda.rs:187-260). */
+/* Backward step 3: with a split-size workspace, dQ = scale * (sum of step 2's partials in
+ * key-block order) into part 0 of dqkv; with a smaller one nothing to do (returns 0). Has no
+ * counterpart launch in the reference (its dQ is summed in place, as the turn mode here). */
+int fattn_bwd_dq_f32_d64(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b,
+                         int64_t h, int64_t s, int64_t d, float scale, int causal, void* stream);
+
+/* All backward steps. Replaces cuda::backward (src/cuda.rs:187-260). */
 int fattn_bwd_f32_d64(const float* q, const float* k, const float* v, const float* o,
                       const float* d_o, const float* lse, float* dqkv, void* workspace,
                       size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,

@@ -298,6 +298,19 @@ def test_kernel_level_entry_points(orc, cuda):
                                   ctypes.byref(status)))
     assert status.value == 0
     assert torch.equal(o, o_ref) and torch.equal(dqkv, g_ref)
+    # The three steps one by one, with either workspace size (causal: both sum dQ in key-block
+    # order, so the results are identical).
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    for size in (L.fattn_bwd_workspace_split_bytes, L.fattn_bwd_workspace_min_bytes):
+        n = size(b, h, s)
+        ws = torch.empty(n, dtype=torch.uint8, device=cuda)
+        dqkv = torch.empty_like(qkv)
+        _lib.check(L.fattn_bwd_prep_f32_d64(P(o), P(wt), gst, P(ws), n, b, h, s, d, stream))
+        _lib.check(L.fattn_bwd_main_f32_d64(qp, kp, vp, P(wt), P(lse), P(dqkv), P(ws), n, b, h,
+                                            s, d, scale, 1, st, st, st, gst, stream))
+        _lib.check(L.fattn_bwd_dq_f32_d64(P(dqkv), P(ws), n, b, h, s, d, scale, 1, stream))
+        torch.cuda.synchronize()
+        assert torch.equal(dqkv, g_ref), f"steps with a {n}-byte workspace"
 
 
 # --- the benchmark configurations -------------------------------
