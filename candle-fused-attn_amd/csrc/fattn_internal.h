@@ -11,7 +11,8 @@ namespace fattn {
 constexpr int kHeadDim = 64;
 
 // Backward tiling: a workgroup owns kBwdKeys keys of one (batch, head) and walks query tiles of
-// kBwdQueryTile; one dQ turn counter per query tile.
+// kBwdQueryTile; per query tile one dQ partial slot per key block (split) or one dQ turn counter
+// (turns).
 constexpr int kBwdKeys = 64;
 #ifndef BWD_QT
 #define BWD_QT 16
