@@ -73,6 +73,17 @@ __device__ __forceinline__ void load_lds16(const float* base, unsigned byte_off,
                : "memory");
 }
 
+// The same for 4 bytes per lane (global_load_lds_dword): lane i's 4 bytes land at `lds_base` + 4 i;
+// inactive lanes write nothing.
+__device__ __forceinline__ void load_lds4(const float* base, unsigned byte_off, float* lds_base) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_float*)lds_base)));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(byte_off), "s"(base), "s"(lds)
+               : "memory");
+}
+
 // Workgroups are handed to the 8 XCDs round-robin (id % 8). This permutation gives each XCD a
 // contiguous range of logical indices, so logical neighbours (same (b, h)) share one L2.
 __device__ __forceinline__ int xcd_remap(int id, int total) {
@@ -461,10 +472,12 @@ bwd_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) float sQ[2][kQT * kHeadDim];
   __shared__ __attribute__((aligned(16))) float sdO[2][kQT * kHeadDim];
   __shared__ __attribute__((aligned(16))) float sdS[kQT * kBwdLd];
-  __shared__ float sL[2][kQT], sD[2][kQT];
+  __shared__ __attribute__((aligned(16))) float sL[2][kQT];
+  __shared__ __attribute__((aligned(16))) float sD[2][kQT];
   __shared__ int s_item;
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lo = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, lo = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
   const int BH = a.B * a.H;
   int item;
   if (kSplit) {
@@ -548,25 +561,17 @@ bwd_kernel(BwdArgs a) {
     kQ[t] = kk < S ? kp[kk * a.k.ss + 16 * w + lo] : 0.0f;
   }
 
-  // Staging of one query tile: wave w copies Q and dO rows kQT / 4 * w .. + kQT / 4 - 1 with
-  // direct copies of four rows each (lane i: row + i / 16, chunk position i % 16, i.e. logical
-  // chunk (i % 16) ^ row); rows past S repeat row S - 1 (finite, masked later). Threads
-  // 0..kQT-1 load L, kQT..2 kQT-1 load D into a register (zero past S), written by sstore.
-  float lst = 0.0f;
-  auto gload = [&](int q0, float* Qdst, float* Gdst) {
-    copy_rows<kQT / 16>(qp, q_ss4, q0, S - 1, Qdst, (kQT / 4) * w, lane);
-    copy_rows<kQT / 16>(gp, g_ss4, q0, S - 1, Gdst, (kQT / 4) * w, lane);
-    if (tid < kQT) {
-      lst = q0 + tid < S ? lp[q0 + tid] : 0.0f;
-    } else if (tid < 2 * kQT) {
-      lst = q0 + tid - kQT < S ? dp[q0 + tid - kQT] : 0.0f;
-    }
-  };
-  auto sstore = [&](int buf) {
-    if (tid < kQT) {
-      sL[buf][tid] = lst;
-    } else if (tid < 2 * kQT) {
-      sD[buf][tid - kQT] = lst;
+  // Staging of one query tile, all by direct copies (nothing passes through registers, so no
+  // wait is needed before the barrier that precedes the tile): wave w copies Q and dO rows
+  // kQT / 4 * w .. + kQT / 4 - 1, four rows per copy (lane i: row + i / 16, chunk position
+  // i % 16, i.e. logical chunk (i % 16) ^ row); wave 0 copies the tile's L, wave 1 its D (lanes
+  // 0..kQT-1, one float each). Rows past S repeat row S - 1 (finite; masked later).
+  auto gload = [&](int q0, int buf) {
+    copy_rows<kQT / 16>(qp, q_ss4, q0, S - 1, sQ[buf], (kQT / 4) * w, lane);
+    copy_rows<kQT / 16>(gp, g_ss4, q0, S - 1, sdO[buf], (kQT / 4) * w, lane);
+    if (w < 2 && lane < kQT) {
+      const unsigned off = 4u * static_cast<unsigned>(min(q0 + lane, S - 1));
+      load_lds4(w == 0 ? lp : dp, off, w == 0 ? sL[buf] : sD[buf]);
     }
   };
   // The order in which key blocks add into a tile's dQ (fixed by the shape alone, so every run
@@ -671,8 +676,7 @@ bwd_kernel(BwdArgs a) {
   };
 
   // Causal: the walk starts at the block's first key (earlier queries see none of its keys).
-  gload(tile_at(0) * kQT, sQ[0], sdO[0]);
-  sstore(0);
+  gload(tile_at(0) * kQT, 0);
   wait_stores();  // the direct copies have landed
   __syncthreads();
   for (int t = 0; t < nsteps; ++t) {
@@ -680,7 +684,7 @@ bwd_kernel(BwdArgs a) {
     const int q0 = tile_at(t) * kQT;
     const bool has_next = t + 1 < nsteps;
     // The next tile into the other buffer, whose last readers passed the last barrier.
-    if (has_next) gload(tile_at(t + 1) * kQT, sQ[buf ^ 1], sdO[buf ^ 1]);
+    if (has_next) gload(tile_at(t + 1) * kQT, buf ^ 1);
     const float* Qt = sQ[buf];
     const float* Gt = sdO[buf];
     int seen = -1;
@@ -733,13 +737,17 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int m = 0; m < kNS; ++m) {
       if (!live[m]) continue;
+      const f4 Lv = ld4(&sL[buf][16 * m + 4 * g]), Dv = ld4(&sD[buf][16 * m + 4 * g]);
+      // Masked: keys past S, queries past S, causal keys after the query (the exponent is finite
+      // for every staged row, and the select drops it).
+      const int qi0 = q0 + 16 * m + 4 * g;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int il = 16 * m + 4 * g + r, qi = q0 + il;
-        const bool ok = qi < S && key < S && !(a.causal && key > qi);
-        const float p = ok ? exp2_hw(fmaf(sS[m][r], a.scale, -sL[buf][il]) * kLog2e) : 0.0f;
-        sP[m][r] = p * (sP[m][r] - sD[buf][il]);  // dS
-        sS[m][r] = p;                              // P
+        const bool ok = qi0 + r < S && key < S && !(a.causal && key > qi0 + r);
+        const float e = exp2_hw(fmaf(sS[m][r], a.scale, -Lv[r]) * kLog2e);
+        const float p = ok ? e : 0.0f;
+        sP[m][r] = p * (sP[m][r] - Dv[r]);  // dS
+        sS[m][r] = p;                        // P
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -805,8 +813,7 @@ bwd_kernel(BwdArgs a) {
     p1_q0 = q0;
     p1_pos = pos_of(q0 / kQT);
     p1_cnt = count_of(q0 / kQT);
-    if (has_next) sstore(buf ^ 1);
-    __syncthreads();  // dS read by every wave; the next tile's L and D staged
+    __syncthreads();  // dS read by every wave
   }
 
   // Drain: the tiles still in the pipeline, in order.
