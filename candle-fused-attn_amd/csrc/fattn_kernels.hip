@@ -39,6 +39,15 @@ namespace fattn {
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+// An int known at compile time, or not, behind the same call syntax.
+template <int V>
+struct Const {
+  __device__ constexpr int operator()() const { return V; }
+};
+struct Var {
+  int v;
+  __device__ int operator()() const { return v; }
+};
 
 constexpr int kThreads = 256;  // 4 waves of 64
 constexpr float kLog2e = 1.44269504088896340736f;
@@ -92,9 +101,20 @@ __device__ __forceinline__ int xcd_remap(int id, int total) {
   return (id & 7) * (full >> 3) + (id >> 3);
 }
 
+// s_waitcnt with vmcnt(n) and no lgkm / export wait (gfx9 encoding: vmcnt bits 3:0 and 15:14,
+// expcnt 6:4, lgkmcnt 11:8). Issued through the builtin, not inline asm, so that the compiler
+// knows which of its own loads have completed: otherwise it adds waits of its own at their first
+// uses -- inside the loops, where they would also wait for the prefetch copies in flight. The
+// empty asm keeps memory accesses from moving across the wait.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt 0..15");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  asm volatile("" ::: "memory");
+}
 // Waits until every vector memory operation of this wave has completed (loads returned, stores
 // and direct copies landed).
-__device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_mem() { wait_vm<0>(); }
 
 // Tiles staged by direct copies are [rows][64 floats], unpadded; the 16-byte chunk c of row r
 // sits at chunk position c ^ (r % 16), which keeps both read patterns used on them
@@ -440,12 +460,12 @@ __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory")
 constexpr int kStage1Loads = 4 * kNS;
 static_assert(kStage1Loads == 4, "wait_except_stage1 encodes vmcnt(4)");
 __device__ __forceinline__ void wait_except_stage1() {
-  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  wait_vm<4>();
 }
 // split: everything but the partial's kNS stores, issued after the next tile's copies.
 static_assert(kNS == 1, "wait_except_part encodes vmcnt(1)");
 __device__ __forceinline__ void wait_except_part() {
-  asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+  wait_vm<1>();
 }
 
 // Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised.
@@ -679,8 +699,11 @@ bwd_kernel(BwdArgs a) {
   gload(tile_at(0) * kQT, 0);
   wait_stores();  // the direct copies have landed
   __syncthreads();
-  for (int t = 0; t < nsteps; ++t) {
-    const int buf = t & 1;
+  // One tile; `bufc()` is the LDS buffer, t % 2. The split kernel unrolls the walk by two so that
+  // it is a compile-time constant there and LDS addresses fold the buffer offset into the
+  // instruction (the turn kernel has no registers to spare for that).
+  auto tile_step = [&](auto bufc, int t) {
+    const int buf = bufc();
     const int q0 = tile_at(t) * kQT;
     const bool has_next = t + 1 < nsteps;
     // The next tile into the other buffer, whose last readers passed the last barrier.
@@ -814,6 +837,14 @@ bwd_kernel(BwdArgs a) {
     p1_pos = pos_of(q0 / kQT);
     p1_cnt = count_of(q0 / kQT);
     __syncthreads();  // dS read by every wave
+  };
+  if constexpr (kSplit) {
+    for (int t = 0; t < nsteps; t += 2) {
+      tile_step(Const<0>{}, t);
+      if (t + 1 < nsteps) tile_step(Const<1>{}, t + 1);
+    }
+  } else {
+    for (int t = 0; t < nsteps; ++t) tile_step(Var{t & 1}, t);
   }
 
   // Drain: the tiles still in the pipeline, in order.
