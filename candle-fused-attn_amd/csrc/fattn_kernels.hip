@@ -65,6 +65,18 @@ __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<con
 __device__ __forceinline__ void st4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
 __device__ __forceinline__ f4 zero4() { return f4{0.0f, 0.0f, 0.0f, 0.0f}; }
 
+// max over lanes lo, lo + 16, lo + 32, lo + 48 (every lane gets it), on the VALU: the gfx950 row
+// swaps pair row r of one operand with row r ^ 1 (16-lane rows), then half h with h ^ 1
+// (32-lane halves); with both operands x, the max of the two results is the max of each pair.
+__device__ __forceinline__ float max4_groups(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const unsigned v = __float_as_uint(x);
+  const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
 typedef __attribute__((address_space(3))) float lds_float;
 // Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane i's 16 bytes land
 // at `lds_base` + 16 i (M0 holds the wave-uniform LDS address). Completion is counted by vmcnt,
@@ -247,8 +259,10 @@ fwd_kernel(FwdArgs a) {
   stage(0, 0);
   wait_mem();
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1, kt0 = t * kFwdKeys;
+  // One key tile; unrolled by two so that the LDS buffer (t % 2) is a compile-time constant and
+  // LDS addresses fold its offset into the instruction.
+  auto tile_step = [&](auto bufc, int t) {
+    const int buf = bufc(), kt0 = t * kFwdKeys;
     // The next tile into the other buffer, whose last readers passed the last barrier.
     if (t + 1 < ntiles) stage(kt0 + kFwdKeys, buf ^ 1);
     if (wave_live) {
@@ -292,8 +306,7 @@ fwd_kernel(FwdArgs a) {
             tmax = fmaxf(tmax, x);
           }
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        tmax = max4_groups(tmax);
         const float m_new = fmaxf(m[n], tmax);
         // A row with every key so far masked keeps m = -inf (exp(-inf - -inf) would be NaN).
         const bool none = m_new == kNegInf;
@@ -329,6 +342,10 @@ fwd_kernel(FwdArgs a) {
     }
     wait_mem();       // the next tile's copies have landed
     __syncthreads();  // and every wave is done with this tile's buffers
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    tile_step(Const<0>{}, t);
+    if (t + 1 < ntiles) tile_step(Const<1>{}, t + 1);
   }
 
   if (wave_live) {
