@@ -293,17 +293,30 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int n = 0; n < kFwdNT; ++n) {
         const int qi = qw0 + 16 * n + lo;
-        // Scale, mask (keys past S; causal keys after the query), tile max.
+        // Scale, mask (keys past S; causal keys after the query), tile max. Non-causal tiles
+        // whose keys are all below S (wave-uniform test) skip the mask.
         float tmax = kNegInf;
+        if (!a.causal && kt0 + kFwdKeys <= S) {
 #pragma unroll
-        for (int mt = 0; mt < kFwdSub; ++mt) {
+          for (int mt = 0; mt < kFwdSub; ++mt) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = kt0 + 16 * mt + 4 * g + r;
-            const bool ok = live[mt] && key < S && !(a.causal && key > qi);
-            const float x = ok ? s[n][mt][r] * a.scale : kNegInf;
-            s[n][mt][r] = x;
-            tmax = fmaxf(tmax, x);
+            for (int r = 0; r < 4; ++r) {
+              const float x = s[n][mt][r] * a.scale;
+              s[n][mt][r] = x;
+              tmax = fmaxf(tmax, x);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < kFwdSub; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = kt0 + 16 * mt + 4 * g + r;
+              const bool ok = live[mt] && key < S && !(a.causal && key > qi);
+              const float x = ok ? s[n][mt][r] * a.scale : kNegInf;
+              s[n][mt][r] = x;
+              tmax = fmaxf(tmax, x);
+            }
           }
         }
         tmax = max4_groups(tmax);
@@ -778,16 +791,26 @@ bwd_kernel(BwdArgs a) {
     for (int m = 0; m < kNS; ++m) {
       if (!live[m]) continue;
       const f4 Lv = ld4(&sL[buf][16 * m + 4 * g]), Dv = ld4(&sD[buf][16 * m + 4 * g]);
-      // Masked: keys past S, queries past S, causal keys after the query (the exponent is finite
-      // for every staged row, and the select drops it).
       const int qi0 = q0 + 16 * m + 4 * g;
+      if (!a.causal && q0 + 16 * m + 16 <= S && kw0 + 16 <= S) {
+        // Every query and key of the subtile is live (wave-uniform test): no mask.
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool ok = qi0 + r < S && key < S && !(a.causal && key > qi0 + r);
-        const float e = exp2_hw(fmaf(sS[m][r], a.scale, -Lv[r]) * kLog2e);
-        const float p = ok ? e : 0.0f;
-        sP[m][r] = p * (sP[m][r] - Dv[r]);  // dS
-        sS[m][r] = p;                        // P
+        for (int r = 0; r < 4; ++r) {
+          const float p = exp2_hw(fmaf(sS[m][r], a.scale, -Lv[r]) * kLog2e);
+          sP[m][r] = p * (sP[m][r] - Dv[r]);  // dS
+          sS[m][r] = p;                        // P
+        }
+      } else {
+        // Masked: keys past S, queries past S, causal keys after the query (the exponent is
+        // finite for every staged row, and the select drops it).
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = qi0 + r < S && key < S && !(a.causal && key > qi0 + r);
+          const float e = exp2_hw(fmaf(sS[m][r], a.scale, -Lv[r]) * kLog2e);
+          const float p = ok ? e : 0.0f;
+          sP[m][r] = p * (sP[m][r] - Dv[r]);  // dS
+          sS[m][r] = p;                        // P
+        }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
