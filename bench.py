@@ -83,7 +83,7 @@ def main() -> int:
     out = torch.empty(B, S, H * D, device=dev)
     lse = torch.empty(B, H, S, device=dev)
     dqkv = torch.empty_like(qkv)
-    ws_bytes = int(L.fattn_bwd_workspace_bytes(B, H, S))
+    ws_bytes = int(L.fattn_bwd_workspace_bytes(B, H, S, D))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
@@ -119,7 +119,7 @@ def main() -> int:
     def dq_k():
         _lib.check(L.fattn_bwd_dq_f32_d64(P(dqkv), P(ws), ws_bytes, B, H, S, D, SCALE, ci, sp))
 
-    split = ws_bytes >= int(L.fattn_bwd_workspace_split_bytes(B, H, S))
+    split = ws_bytes >= int(L.fattn_bwd_workspace_split_bytes(B, H, S, D))
 
     if args.calibrate_copy:
         src = torch.ones(64 * 1024 * 1024, device=dev)   # 256 MiB

@@ -1,5 +1,6 @@
-"""candle_fused_attn on MI355X: fused fp32 scaled-dot-product attention, head_dim 64, forward and
-deterministic backward, on hand-written gfx950 kernels (libfattn.so).
+"""candle_fused_attn on MI355X: fused fp32 scaled-dot-product attention, forward and
+deterministic backward, head_dim 32, 64 or 128 (the reference's is 64), on hand-written gfx950
+kernels (libfattn.so).
 
 The public surface mirrors the reference crate's (src/lib.rs:90-161): `fused_attention`,
 `fused_attention_qkv`, `CUDA_HEAD_DIM`.
@@ -8,6 +9,7 @@ from ._lib import FusedAttentionError, LIB_PATH, version
 from .ops import (
     CUDA_HEAD_DIM,
     HIP_HEAD_DIM,
+    HIP_HEAD_DIMS,
     float4_aligned,
     fused_attention,
     fused_attention_qkv,
@@ -18,6 +20,7 @@ from .ops import (
 __all__ = [
     "CUDA_HEAD_DIM",
     "HIP_HEAD_DIM",
+    "HIP_HEAD_DIMS",
     "FusedAttentionError",
     "LIB_PATH",
     "float4_aligned",

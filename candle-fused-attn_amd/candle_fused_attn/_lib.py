@@ -21,10 +21,15 @@ FATTN_EWORKSPACE = -5
 
 # Every entry point include/fattn.h declares.
 EXPORTS = (
-    "fattn_fwd_f32_d64",
+    "fattn_fwd_f32",
     "fattn_bwd_workspace_bytes",
     "fattn_bwd_workspace_min_bytes",
     "fattn_bwd_workspace_split_bytes",
+    "fattn_bwd_prep_f32",
+    "fattn_bwd_main_f32",
+    "fattn_bwd_dq_f32",
+    "fattn_bwd_f32",
+    "fattn_fwd_f32_d64",
     "fattn_bwd_prep_f32_d64",
     "fattn_bwd_main_f32_d64",
     "fattn_bwd_dq_f32_d64",
@@ -65,16 +70,20 @@ def _declare(L: ctypes.CDLL) -> None:
     L.fattn_version.restype = ctypes.c_char_p
     for name in ("fattn_bwd_workspace_bytes", "fattn_bwd_workspace_min_bytes",
                  "fattn_bwd_workspace_split_bytes"):
-        getattr(L, name).argtypes = [I64, I64, I64]
+        getattr(L, name).argtypes = [I64, I64, I64, I64]
         getattr(L, name).restype = SIZE
-    L.fattn_fwd_f32_d64.argtypes = [P, P, P, P, P, I64, I64, I64, I64, C_FLOAT, C_INT, A3, A3,
-                                    A3, P]
-    L.fattn_bwd_prep_f32_d64.argtypes = [P, P, A3, P, SIZE, I64, I64, I64, I64, P]
-    L.fattn_bwd_main_f32_d64.argtypes = [P, P, P, P, P, P, P, SIZE, I64, I64, I64, I64, C_FLOAT,
-                                         C_INT, A3, A3, A3, A3, P]
-    L.fattn_bwd_dq_f32_d64.argtypes = [P, P, SIZE, I64, I64, I64, I64, C_FLOAT, C_INT, P]
-    L.fattn_bwd_f32_d64.argtypes = [P, P, P, P, P, P, P, P, SIZE, I64, I64, I64, I64, C_FLOAT,
-                                    C_INT, A3, A3, A3, A3, P]
+    for sfx in ("", "_d64"):
+        getattr(L, "fattn_fwd_f32" + sfx).argtypes = [P, P, P, P, P, I64, I64, I64, I64, C_FLOAT,
+                                                      C_INT, A3, A3, A3, P]
+        getattr(L, "fattn_bwd_prep_f32" + sfx).argtypes = [P, P, A3, P, SIZE, I64, I64, I64, I64,
+                                                           P]
+        getattr(L, "fattn_bwd_main_f32" + sfx).argtypes = [P, P, P, P, P, P, P, SIZE, I64, I64,
+                                                           I64, I64, C_FLOAT, C_INT, A3, A3, A3,
+                                                           A3, P]
+        getattr(L, "fattn_bwd_dq_f32" + sfx).argtypes = [P, P, SIZE, I64, I64, I64, I64, C_FLOAT,
+                                                         C_INT, P]
+        getattr(L, "fattn_bwd_f32" + sfx).argtypes = [P, P, P, P, P, P, P, P, SIZE, I64, I64, I64,
+                                                      I64, C_FLOAT, C_INT, A3, A3, A3, A3, P]
     L.fattn_qkv_forward.argtypes = [P, I64, A3, A3, I64, C_FLOAT, C_INT, P, P, P]
     L.fattn_qkv_backward.argtypes = [P, I64, A3, A3, I64, C_FLOAT, C_INT, P, P, P, I64, A3, A3,
                                      P, P, SIZE, P]

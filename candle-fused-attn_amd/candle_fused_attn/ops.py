@@ -26,8 +26,10 @@ import torch
 from . import _lib
 from ._lib import FusedAttentionError, arr, check
 
-# The head dimension the kernels are built for (src/lib.rs:91, CUDA_HEAD_DIM).
+# The reference's head dimension (src/lib.rs:91, CUDA_HEAD_DIM), and those the kernels here are
+# built for.
 CUDA_HEAD_DIM = 64
+HIP_HEAD_DIMS = (32, 64, 128)
 HIP_HEAD_DIM = CUDA_HEAD_DIM
 
 
@@ -124,11 +126,11 @@ def set_dq_sum(mode: str) -> str:
     return prev
 
 
-def _workspace(b: int, h: int, s: int, device: torch.device) -> torch.Tensor:
+def _workspace(b: int, h: int, s: int, d: int, device: torch.device) -> torch.Tensor:
     L = _lib.lib()
     size = {"auto": L.fattn_bwd_workspace_bytes, "split": L.fattn_bwd_workspace_split_bytes,
             "turns": L.fattn_bwd_workspace_min_bytes}[_dq_sum]
-    nbytes = int(size(b, h, s))
+    nbytes = int(size(b, h, s, d))
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
@@ -161,7 +163,7 @@ class _FusedAttentionQkv(torch.autograd.Function):
         grad = _aligned_grad(grad)
         b, s, three_hd = qkv.shape
         dqkv = torch.empty((b, s, three_hd), dtype=torch.float32, device=qkv.device)
-        ws = _workspace(b, ctx.heads, s, qkv.device)
+        ws = _workspace(b, ctx.heads, s, three_hd // 3 // max(ctx.heads, 1), qkv.device)
         base, off = _storage(qkv)
         gbase, goff = _storage(grad)
         check(_lib.lib().fattn_qkv_backward(
@@ -203,7 +205,7 @@ class _FusedAttention(torch.autograd.Function):
         grad = _aligned_grad(grad)
         b, h, s, d = q.shape
         dqkv = torch.empty((b, s, 3, h, d), dtype=torch.float32, device=q.device)
-        ws = _workspace(b, h, s, q.device)
+        ws = _workspace(b, h, s, d, q.device)
         (qb, qo), (kb, ko), (vb, vo) = _storage(q), _storage(k), _storage(v)
         gbase, goff = _storage(grad)
         check(_lib.lib().fattn_backward(

@@ -14,7 +14,7 @@
 
 namespace fattn {
 
-Workspace workspace_layout(int64_t b, int64_t h, int64_t s) {
+Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d) {
   auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   Workspace w{};
   const size_t rows = static_cast<size_t>(b * h * s);
@@ -25,7 +25,8 @@ Workspace workspace_layout(int64_t b, int64_t h, int64_t s) {
   w.ctrl_off = w.turn_off + up(tiles * sizeof(int));
   w.part_off = w.ctrl_off + up(64 * sizeof(int));
   w.bytes_min = w.part_off;
-  w.bytes_split = w.part_off + up(nkb * tiles * kBwdQueryTile * kHeadDim * sizeof(float));
+  w.bytes_split = w.part_off + up(nkb * tiles * kBwdQueryTile * static_cast<size_t>(d) *
+                                  sizeof(float));
   return w;
 }
 
@@ -66,7 +67,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // Kernel index range: every (b, h, s) index product and the grid stay inside int32, and the
 // launch inside 2^32 threads.
-int check_range(const char* who, int64_t b, int64_t h, int64_t s) {
+int check_range(const char* who, int64_t b, int64_t h, int64_t s, int64_t d) {
   const int64_t lim = INT32_MAX;
   if (b > lim || h > lim || s > lim || b * h > lim || b * h * s > lim) {
     return fail(FATTN_ERANGE, std::string(who) + ": " + std::to_string(b) + " x " +
@@ -74,8 +75,11 @@ int check_range(const char* who, int64_t b, int64_t h, int64_t s) {
                                   " exceeds i32 indexing");
   }
   const int64_t grid_lim = (int64_t{1} << 32) / 256 - 1;
-  if (fattn::forward_blocks(b, h, s, 1) > grid_lim || fattn::bwd_main_blocks(b, h, s) > grid_lim ||
-      fattn::bwd_prep_blocks(b, h, s) > grid_lim) {
+  const int dd = static_cast<int>(d);
+  if (fattn::forward_blocks(b, h, s, 1, dd) > grid_lim ||
+      fattn::forward_blocks(b, h, s, 0, dd) > grid_lim ||
+      fattn::bwd_main_blocks(b, h, s) > grid_lim || fattn::bwd_prep_blocks(b, h, s, dd) > grid_lim ||
+      fattn::bwd_dq_blocks(b, h, s) > grid_lim) {
     return fail(FATTN_ERANGE, std::string(who) + ": the grid for " + std::to_string(b) +
                                   " x " + std::to_string(h) + " x " + std::to_string(s) +
                                   " exceeds the launch limit");
@@ -83,7 +87,19 @@ int check_range(const char* who, int64_t b, int64_t h, int64_t s) {
   return 0;
 }
 
+// The op level and the generic kernel-level entries: the head_dims the kernels are built for.
 int check_head_dim(int64_t d) {
+  if (!fattn::head_dim_supported(d)) {
+    return fail(FATTN_EHEADDIM,
+                "fused_attention: the HIP kernels take head_dim 32, 64 or 128, got " +
+                    std::to_string(d));
+  }
+  return 0;
+}
+
+// The entries named after the reference's d64 kernels take exactly its head_dim
+// (src/cuda.rs:85-93).
+int check_head_dim64(int64_t d) {
   if (d != fattn::kHeadDim) {
     return fail(FATTN_EHEADDIM, "fused_attention: the HIP kernels take head_dim 64, got " +
                                     std::to_string(d));
@@ -99,8 +115,8 @@ View make_view(const float* base, const int64_t st[3]) { return View{base, st[0]
 
 // The kernels address a (b, h) slice of an operand (and a batch of dqkv) with 32-bit byte or
 // element offsets from a per-slice base.
-bool slice_fits(const View& v, int64_t s) {
-  return (s - 1) * v.ss * 4 + 4 * fattn::kHeadDim <= int64_t{UINT32_MAX};
+bool slice_fits(const View& v, int64_t s, int64_t d) {
+  return (s - 1) * v.ss * 4 + 4 * d <= int64_t{UINT32_MAX};
 }
 
 int slice_error(const char* who, int64_t s) {
@@ -110,18 +126,18 @@ int slice_error(const char* who, int64_t s) {
 
 // Shared body of the kernel-level forward.
 int run_forward(const char* who, View q, View k, View v, float* o, float* lse, int64_t b,
-                int64_t h, int64_t s, float scale, int causal, void* stream) {
-  if (int rc = check_range(who, b, h, s)) return rc;
+                int64_t h, int64_t s, int64_t d, float scale, int causal, void* stream) {
+  if (int rc = check_range(who, b, h, s, d)) return rc;
   if (!q.p || !k.p || !v.p || !o || !lse) {
     return fail(FATTN_EINVAL, std::string(who) + ": null operand");
   }
   if (!view_aligned(q) || !view_aligned(k) || !view_aligned(v) || !aligned16(o)) {
     return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
   }
-  if (!slice_fits(k, s) || !slice_fits(v, s)) return slice_error(who, s);
+  if (!slice_fits(k, s, d) || !slice_fits(v, s, d)) return slice_error(who, s);
   const int err = fattn::launch_forward(q, k, v, o, lse, static_cast<int>(b),
-                                        static_cast<int>(h), static_cast<int>(s), scale,
-                                        causal ? 1 : 0, stream);
+                                        static_cast<int>(h), static_cast<int>(s),
+                                        static_cast<int>(d), scale, causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "forward launch");
   return ok();
 }
@@ -134,8 +150,8 @@ struct WsParts {
 };
 
 int workspace_parts(const char* who, void* ws, size_t ws_bytes, int64_t b, int64_t h, int64_t s,
-                    WsParts* out) {
-  const fattn::Workspace l = fattn::workspace_layout(b, h, s);
+                    int64_t d, WsParts* out) {
+  const fattn::Workspace l = fattn::workspace_layout(b, h, s, d);
   if (!ws || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0 || ws_bytes < l.bytes_min) {
     return fail(FATTN_EWORKSPACE, std::string(who) + ": the backward needs a 256-byte aligned " +
                                       "workspace of at least " + std::to_string(l.bytes_min) +
@@ -150,26 +166,26 @@ int workspace_parts(const char* who, void* ws, size_t ws_bytes, int64_t b, int64
 }
 
 int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_bytes, int64_t b,
-                 int64_t h, int64_t s, void* stream) {
-  if (int rc = check_range(who, b, h, s)) return rc;
+                 int64_t h, int64_t s, int64_t d, void* stream) {
+  if (int rc = check_range(who, b, h, s, d)) return rc;
   if (!o || !d_o.p) return fail(FATTN_EINVAL, std::string(who) + ": null operand");
   if (!aligned16(o) || !view_aligned(d_o)) {
     return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
   }
   WsParts p{};
-  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, &p)) return rc;
+  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
   const int err = fattn::launch_bwd_prep(o, d_o, p.dsum, p.turn, p.ctrl, static_cast<int>(b),
-                                         static_cast<int>(h), static_cast<int>(s), stream);
+                                         static_cast<int>(h), static_cast<int>(s),
+                                         static_cast<int>(d), stream);
   if (err) return hip_fail(err, "backward step 1 launch");
   return ok();
 }
 
 int run_bwd_main(const char* who, View q, View k, View v, View d_o, const float* lse,
                  float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h, int64_t s,
-                 float scale, int causal, void* stream) {
-  if (int rc = check_range(who, b, h, s)) return rc;
-  if (!slice_fits(q, s) || !slice_fits(d_o, s) ||
-      s * 3 * h * fattn::kHeadDim > int64_t{UINT32_MAX}) {
+                 int64_t d, float scale, int causal, void* stream) {
+  if (int rc = check_range(who, b, h, s, d)) return rc;
+  if (!slice_fits(q, s, d) || !slice_fits(d_o, s, d) || s * 3 * h * d > int64_t{UINT32_MAX}) {
     return slice_error(who, s);
   }
   if (!q.p || !k.p || !v.p || !d_o.p || !lse || !dqkv) {
@@ -180,41 +196,43 @@ int run_bwd_main(const char* who, View q, View k, View v, View d_o, const float*
     return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
   }
   WsParts p{};
-  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, &p)) return rc;
+  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
   const int err = fattn::launch_bwd_main(q, k, v, d_o, lse, p.dsum, dqkv, p.part, p.turn, p.ctrl,
                                          static_cast<int>(b), static_cast<int>(h),
-                                         static_cast<int>(s), scale, causal ? 1 : 0, stream);
+                                         static_cast<int>(s), static_cast<int>(d), scale,
+                                         causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 2 launch");
   return ok();
 }
 
 // Step 3: in split mode (the workspace holds the partials) dQ from the partials; else nothing.
 int run_bwd_dq(const char* who, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
-               int64_t s, float scale, int causal, void* stream) {
-  if (int rc = check_range(who, b, h, s)) return rc;
-  if (s * 3 * h * fattn::kHeadDim > int64_t{UINT32_MAX}) return slice_error(who, s);
+               int64_t s, int64_t d, float scale, int causal, void* stream) {
+  if (int rc = check_range(who, b, h, s, d)) return rc;
+  if (s * 3 * h * d > int64_t{UINT32_MAX}) return slice_error(who, s);
   if (!dqkv) return fail(FATTN_EINVAL, std::string(who) + ": null operand");
   if (!aligned16(dqkv)) {
     return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
   }
   WsParts p{};
-  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, &p)) return rc;
+  if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
   if (!p.part) return ok();
   const int err = fattn::launch_bwd_dq(p.part, dqkv, static_cast<int>(b), static_cast<int>(h),
-                                       static_cast<int>(s), scale, causal ? 1 : 0, stream);
+                                       static_cast<int>(s), static_cast<int>(d), scale,
+                                       causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 3 launch");
   return ok();
 }
 
 int run_backward(const char* who, View q, View k, View v, const float* o, View d_o,
                  const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
-                 int64_t s, float scale, int causal, void* stream) {
-  if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, stream)) return rc;
-  if (int rc = run_bwd_main(who, q, k, v, d_o, lse, dqkv, ws, ws_bytes, b, h, s, scale, causal,
+                 int64_t s, int64_t d, float scale, int causal, void* stream) {
+  if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, d, stream)) return rc;
+  if (int rc = run_bwd_main(who, q, k, v, d_o, lse, dqkv, ws, ws_bytes, b, h, s, d, scale, causal,
                             stream)) {
     return rc;
   }
-  return run_bwd_dq(who, dqkv, ws, ws_bytes, b, h, s, scale, causal, stream);
+  return run_bwd_dq(who, dqkv, ws, ws_bytes, b, h, s, d, scale, causal, stream);
 }
 
 bool negative(const int64_t* x, int n) {
@@ -281,28 +299,30 @@ extern "C" {
 
 const char* fattn_last_error(void) { return g_error.c_str(); }
 
-const char* fattn_version(void) { return "fattn-gfx950 0.1.0 (head_dim 64, fp32 MFMA)"; }
+const char* fattn_version(void) {
+  return "fattn-gfx950 0.2.0 (head_dim 32, 64, 128; fp32 MFMA)";
+}
 
-size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s) {
-  if (b < 0 || h < 0 || s < 0) return 0;
-  const fattn::Workspace l = fattn::workspace_layout(b, h, s);
+size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s, int64_t d) {
+  if (b < 0 || h < 0 || s < 0 || !fattn::head_dim_supported(d)) return 0;
+  const fattn::Workspace l = fattn::workspace_layout(b, h, s, d);
   return l.bytes_split <= FATTN_SPLIT_MAX_BYTES ? l.bytes_split : l.bytes_min;
 }
 
-size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s) {
-  if (b < 0 || h < 0 || s < 0) return 0;
-  return fattn::workspace_layout(b, h, s).bytes_min;
+size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s, int64_t d) {
+  if (b < 0 || h < 0 || s < 0 || !fattn::head_dim_supported(d)) return 0;
+  return fattn::workspace_layout(b, h, s, d).bytes_min;
 }
 
-size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s) {
-  if (b < 0 || h < 0 || s < 0) return 0;
-  return fattn::workspace_layout(b, h, s).bytes_split;
+size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s, int64_t d) {
+  if (b < 0 || h < 0 || s < 0 || !fattn::head_dim_supported(d)) return 0;
+  return fattn::workspace_layout(b, h, s, d).bytes_split;
 }
 
-int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,
-                      int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
-                      const int64_t q_strides[3], const int64_t k_strides[3],
-                      const int64_t v_strides[3], void* stream) {
+int fattn_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse, int64_t b,
+                  int64_t h, int64_t s, int64_t d, float scale, int causal,
+                  const int64_t q_strides[3], const int64_t k_strides[3],
+                  const int64_t v_strides[3], void* stream) {
   if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
   if (int rc = check_head_dim(d)) return rc;
   if (empty3(b, h, s)) return ok();
@@ -310,26 +330,25 @@ int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, 
     return fail(FATTN_EINVAL, "fused_attention: null strides");
   }
   return run_forward("fused_attention", make_view(q, q_strides), make_view(k, k_strides),
-                     make_view(v, v_strides), o, lse, b, h, s, scale, causal, stream);
+                     make_view(v, v_strides), o, lse, b, h, s, d, scale, causal, stream);
 }
 
-int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_strides[3],
-                           void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
-                           int64_t s, int64_t d, void* stream) {
+int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_strides[3],
+                       void* workspace, size_t workspace_bytes, int64_t b, int64_t h, int64_t s,
+                       int64_t d, void* stream) {
   if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
   if (int rc = check_head_dim(d)) return rc;
   if (empty3(b, h, s)) return ok();
   if (!do_strides) return fail(FATTN_EINVAL, "fused_attention: null strides");
   return run_bwd_prep("fused_attention", o, make_view(d_o, do_strides), workspace,
-                      workspace_bytes, b, h, s, stream);
+                      workspace_bytes, b, h, s, d, stream);
 }
 
-int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
-                           const float* lse, float* dqkv, void* workspace,
-                           size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
-                           float scale, int causal, const int64_t q_strides[3],
-                           const int64_t k_strides[3], const int64_t v_strides[3],
-                           const int64_t do_strides[3], void* stream) {
+int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* d_o,
+                       const float* lse, float* dqkv, void* workspace, size_t workspace_bytes,
+                       int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
+                       const int64_t q_strides[3], const int64_t k_strides[3],
+                       const int64_t v_strides[3], const int64_t do_strides[3], void* stream) {
   if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
   if (int rc = check_head_dim(d)) return rc;
   if (empty3(b, h, s)) return ok();
@@ -338,24 +357,24 @@ int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const
   }
   return run_bwd_main("fused_attention", make_view(q, q_strides), make_view(k, k_strides),
                       make_view(v, v_strides), make_view(d_o, do_strides), lse, dqkv, workspace,
-                      workspace_bytes, b, h, s, scale, causal, stream);
+                      workspace_bytes, b, h, s, d, scale, causal, stream);
 }
 
-int fattn_bwd_dq_f32_d64(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b,
-                         int64_t h, int64_t s, int64_t d, float scale, int causal, void* stream) {
+int fattn_bwd_dq_f32(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
+                     int64_t s, int64_t d, float scale, int causal, void* stream) {
   if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
   if (int rc = check_head_dim(d)) return rc;
   if (empty3(b, h, s)) return ok();
-  return run_bwd_dq("fused_attention", dqkv, workspace, workspace_bytes, b, h, s, scale, causal,
-                    stream);
+  return run_bwd_dq("fused_attention", dqkv, workspace, workspace_bytes, b, h, s, d, scale,
+                    causal, stream);
 }
 
-int fattn_bwd_f32_d64(const float* q, const float* k, const float* v, const float* o,
-                      const float* d_o, const float* lse, float* dqkv, void* workspace,
-                      size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
-                      float scale, int causal, const int64_t q_strides[3],
-                      const int64_t k_strides[3], const int64_t v_strides[3],
-                      const int64_t do_strides[3], void* stream) {
+int fattn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
+                  const float* d_o, const float* lse, float* dqkv, void* workspace,
+                  size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                  float scale, int causal, const int64_t q_strides[3],
+                  const int64_t k_strides[3], const int64_t v_strides[3],
+                  const int64_t do_strides[3], void* stream) {
   if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
   if (int rc = check_head_dim(d)) return rc;
   if (empty3(b, h, s)) return ok();
@@ -364,7 +383,52 @@ int fattn_bwd_f32_d64(const float* q, const float* k, const float* v, const floa
   }
   return run_backward("fused_attention", make_view(q, q_strides), make_view(k, k_strides),
                       make_view(v, v_strides), o, make_view(d_o, do_strides), lse, dqkv,
-                      workspace, workspace_bytes, b, h, s, scale, causal, stream);
+                      workspace, workspace_bytes, b, h, s, d, scale, causal, stream);
+}
+
+// The reference-named head_dim-64 entries: the generic ones behind the reference's check.
+int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,
+                      int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
+                      const int64_t q_strides[3], const int64_t k_strides[3],
+                      const int64_t v_strides[3], void* stream) {
+  if (int rc = check_head_dim64(d)) return rc;
+  return fattn_fwd_f32(q, k, v, o, lse, b, h, s, d, scale, causal, q_strides, k_strides,
+                       v_strides, stream);
+}
+
+int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_strides[3],
+                           void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
+                           int64_t s, int64_t d, void* stream) {
+  if (int rc = check_head_dim64(d)) return rc;
+  return fattn_bwd_prep_f32(o, d_o, do_strides, workspace, workspace_bytes, b, h, s, d, stream);
+}
+
+int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
+                           const float* lse, float* dqkv, void* workspace,
+                           size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                           float scale, int causal, const int64_t q_strides[3],
+                           const int64_t k_strides[3], const int64_t v_strides[3],
+                           const int64_t do_strides[3], void* stream) {
+  if (int rc = check_head_dim64(d)) return rc;
+  return fattn_bwd_main_f32(q, k, v, d_o, lse, dqkv, workspace, workspace_bytes, b, h, s, d,
+                            scale, causal, q_strides, k_strides, v_strides, do_strides, stream);
+}
+
+int fattn_bwd_dq_f32_d64(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b,
+                         int64_t h, int64_t s, int64_t d, float scale, int causal, void* stream) {
+  if (int rc = check_head_dim64(d)) return rc;
+  return fattn_bwd_dq_f32(dqkv, workspace, workspace_bytes, b, h, s, d, scale, causal, stream);
+}
+
+int fattn_bwd_f32_d64(const float* q, const float* k, const float* v, const float* o,
+                      const float* d_o, const float* lse, float* dqkv, void* workspace,
+                      size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                      float scale, int causal, const int64_t q_strides[3],
+                      const int64_t k_strides[3], const int64_t v_strides[3],
+                      const int64_t do_strides[3], void* stream) {
+  if (int rc = check_head_dim64(d)) return rc;
+  return fattn_bwd_f32(q, k, v, o, d_o, lse, dqkv, workspace, workspace_bytes, b, h, s, d, scale,
+                       causal, q_strides, k_strides, v_strides, do_strides, stream);
 }
 
 int fattn_qkv_forward(const float* qkv, int64_t offset, const int64_t shape[3],
@@ -383,7 +447,7 @@ int fattn_qkv_forward(const float* qkv, int64_t offset, const int64_t shape[3],
   const View q{base, strides[0], d, strides[1]};
   const View k{base + hd, strides[0], d, strides[1]};
   const View v{base + 2 * hd, strides[0], d, strides[1]};
-  return run_forward("fused_attention_qkv", q, k, v, out, lse, b, heads, s, scale, causal,
+  return run_forward("fused_attention_qkv", q, k, v, out, lse, b, heads, s, d, scale, causal,
                      stream);
 }
 
@@ -420,7 +484,7 @@ int fattn_qkv_backward(const float* qkv, int64_t offset, const int64_t shape[3],
   const View v{base + 2 * hd, strides[0], d, strides[1]};
   const View g{grad + grad_offset, grad_strides[0], d, grad_strides[1]};
   return run_backward("fused_attention_qkv", q, k, v, out, g, lse, dqkv, workspace,
-                      workspace_bytes, b, heads, s, scale, causal, stream);
+                      workspace_bytes, b, heads, s, d, scale, causal, stream);
 }
 
 int fattn_forward(const float* q, int64_t q_offset, const int64_t q_shape[4],
@@ -432,7 +496,7 @@ int fattn_forward(const float* q, int64_t q_offset, const int64_t q_shape[4],
     return rc;
   }
   if (int rc = check_head_dim(q_shape[3])) return rc;
-  const int64_t b = q_shape[0], h = q_shape[1], s = q_shape[2];
+  const int64_t b = q_shape[0], h = q_shape[1], s = q_shape[2], d = q_shape[3];
   if (empty3(b, h, s)) return ok();
   if (!q || !k || !v || q_offset < 0 || k_offset < 0 || v_offset < 0) {
     return fail(FATTN_EINVAL, "fused_attention: null operand");
@@ -440,7 +504,7 @@ int fattn_forward(const float* q, int64_t q_offset, const int64_t q_shape[4],
   const View qv{q + q_offset, q_strides[0], q_strides[1], q_strides[2]};
   const View kv{k + k_offset, k_strides[0], k_strides[1], k_strides[2]};
   const View vv{v + v_offset, v_strides[0], v_strides[1], v_strides[2]};
-  return run_forward("fused_attention", qv, kv, vv, out, lse, b, h, s, scale, causal, stream);
+  return run_forward("fused_attention", qv, kv, vv, out, lse, b, h, s, d, scale, causal, stream);
 }
 
 int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
@@ -476,7 +540,7 @@ int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
   const View vv{v + v_offset, v_strides[0], v_strides[1], v_strides[2]};
   const View g{grad + grad_offset, grad_strides[0], grad_strides[2], grad_strides[1]};
   return run_backward("fused_attention", qv, kv, vv, out, g, lse, dqkv, workspace,
-                      workspace_bytes, b, h, s, scale, causal, stream);
+                      workspace_bytes, b, h, s, d, scale, causal, stream);
 }
 
 int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
@@ -485,8 +549,9 @@ int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, i
   *status = 0;
   if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
   WsParts p{};
+  // The guard word's place does not depend on head_dim.
   if (int rc = workspace_parts("fused_attention", const_cast<void*>(workspace), workspace_bytes,
-                               b, h, s, &p)) {
+                               b, h, s, fattn::kHeadDim, &p)) {
     return rc;
   }
   hipError_t err = hipStreamSynchronize(static_cast<hipStream_t>(stream));

@@ -8,7 +8,9 @@
 
 namespace fattn {
 
+// head_dim of the reference's kernels; the kernels here are built for 32, 64 and 128.
 constexpr int kHeadDim = 64;
+bool head_dim_supported(int64_t d);
 
 // Backward tiling: a workgroup owns kBwdKeys keys of one (batch, head) and walks query tiles of
 // kBwdQueryTile; per query tile one dQ partial slot per key block (split) or one dQ turn counter
@@ -19,7 +21,7 @@ constexpr int kBwdKeys = 64;
 #endif
 constexpr int kBwdQueryTile = BWD_QT;
 
-// A [b, h, s, 64] operand on the device: its first element and its (batch, head, seq) strides
+// A [b, h, s, d] operand on the device: its first element and its (batch, head, seq) strides
 // in floats, head_dim contiguous.
 struct View {
   const float* p;
@@ -30,34 +32,34 @@ struct View {
 //   D      [b, h, s] f32                    rowsum(dO o O)
 //   turn   [b, h, ntile] i32                dQ turn counter per query tile (turn hand-over)
 //   ctrl   64 i32                           [0] key-block ticket, [32] guard word
-//   part   [nkb, b, h, ntile, kQT * 64] f32 dQ partial per key block and query tile (split only)
+//   part   [nkb, b, h, ntile, kQT * d] f32 dQ partial per key block and query tile (split only)
 // with ntile = ceil(s / kBwdQueryTile), nkb = ceil(s / kBwdKeys). `bytes_min` covers D, turn and
 // ctrl (the turn hand-over), `bytes_split` all four.
 struct Workspace {
   size_t d_off, turn_off, ctrl_off, part_off, bytes_min, bytes_split;
 };
-Workspace workspace_layout(int64_t b, int64_t h, int64_t s);
+Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d);
 constexpr int kCtrlTicket = 0;
 constexpr int kCtrlGuard = 32;
 
 // Launchers (fattn_kernels.hip). They assume validated arguments; they return a hipError_t
 // value as int (0 = launched).
-int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s,
+int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s, int d,
                    float scale, int causal, void* stream);
 int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl, int b, int h,
-                    int s, void* stream);
+                    int s, int d, void* stream);
 // part == nullptr: the turn hand-over (dQ final after step 2); else the split partials, which
 // step 3 (launch_bwd_dq) sums into dQ.
 int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
-                    float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s,
+                    float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s, int d,
                     float scale, int causal, void* stream);
-int launch_bwd_dq(const float* part, float* dqkv, int b, int h, int s, float scale, int causal,
-                  void* stream);
+int launch_bwd_dq(const float* part, float* dqkv, int b, int h, int s, int d, float scale,
+                  int causal, void* stream);
 
 // Grid sizes the launchers will use (for range checks before launching).
-int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal);
+int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal, int d);
 int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s);
-int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s);
+int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d);
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s);
 
 }  // namespace fattn

@@ -1,4 +1,5 @@
-// Fused fp32 scaled-dot-product attention for gfx950 (MI355X / CDNA4), head_dim 64: a
+// Fused fp32 scaled-dot-product attention for gfx950 (MI355X / CDNA4), head_dim D = 32, 64 or 128
+// (every kernel is a template on D; 64 is the reference's, 32 and 128 its roadmap's): a
 // FlashAttention-2-style forward (online softmax, the [s, s] scores never written, only O and the
 // row log-sum-exp L stored) and a deterministic one-pass backward.
 //
@@ -17,8 +18,8 @@
 //     but one max exchange per tile.
 //
 // Layouts (element offsets; strides in floats): q, k, v and dO are read through (batch, head,
-// seq) strides with head_dim contiguous, every row 16-byte aligned; O is written [b, s, h, 64];
-// L and D are [b, h, s]; dQ, dK, dV are written interleaved into one [b, s, 3, h, 64] buffer.
+// seq) strides with head_dim contiguous, every row 16-byte aligned; O is written [b, s, h, D];
+// L and D are [b, h, s]; dQ, dK, dV are written interleaved into one [b, s, 3, h, D] buffer.
 //
 // Determinism: every sum has an order fixed by the shape alone. The cross-workgroup sum (dQ over
 // key blocks) is done one of two ways, chosen by the size of the caller's workspace:
@@ -128,41 +129,50 @@ __device__ __forceinline__ void wait_vm() {
 // and direct copies landed).
 __device__ __forceinline__ void wait_mem() { wait_vm<0>(); }
 
-// Tiles staged by direct copies are [rows][64 floats], unpadded; the 16-byte chunk c of row r
-// sits at chunk position c ^ (r % 16), which keeps both read patterns used on them
-// conflict-free: row-wise float4 reads (16 lanes, 16 rows, one chunk each) and column reads
-// (lanes across 4 rows x 16 consecutive floats).
+// Tiles staged by direct copies are [rows][D floats], unpadded, in 16-byte chunks; chunk c of row
+// r sits at position c ^ f(r), which keeps both read patterns used on them free of bank
+// conflicts: row-wise float4 reads (16 lanes on 16 rows, the same chunk each: the 16 positions
+// must fall in distinct 16-byte bank groups of 256 bytes) and column reads (lanes across 4 rows x
+// 16 consecutive floats). f(r) = r % 16 for D 64 and 128 (rows are multiples of 256 bytes);
+// D 32 (128-byte rows: two rows per 256 bytes) uses f(r) = (r / 2) % 8, conflict-free for the row
+// reads, 2-way for the column reads (64 lanes over 4 rows of 128 bytes cannot do better).
+template <int D>
+__device__ __forceinline__ int swz_f(int row) {
+  return D == 32 ? ((row >> 1) & 7) : (row & 15);
+}
+template <int D>
 __device__ __forceinline__ int swz(int row, int col) {
-  return row * kHeadDim + ((((col >> 2) ^ row) & 15) << 2) + (col & 3);
+  return row * D + ((((col >> 2) ^ swz_f<D>(row)) & (D / 4 - 1)) << 2) + (col & 3);
 }
 
-// Copy rows [row0, row0 + 4 n) of a [rows][64] tile from global (base + row * row_bytes, rows past
-// `last` repeat row `last`) into the swizzled LDS tile `dst`, n direct copies of 4 rows per wave:
-// lane i moves chunk position i % 16 of row row0 + 4 j + i / 16, i.e. logical chunk
-// (i % 16) ^ row.
-template <int N>
-__device__ __forceinline__ void copy_rows(const float* base, unsigned row_bytes, int first_row,
-                                          int last_row, float* dst, int row0, int lane) {
-#pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const int row = row0 + 4 * j + (lane >> 4);
-    const unsigned src_row = static_cast<unsigned>(min(first_row + row, last_row));
-    const unsigned c16 = 16u * static_cast<unsigned>((lane & 15) ^ (row & 15));
-    load_lds16(base, src_row * row_bytes + c16, dst + (row0 + 4 * j) * kHeadDim);
-  }
+// One direct copy of 1024 bytes (16 per lane) of a [rows][D] tile: rows kCopyRows j ..
+// kCopyRows (j + 1) - 1 from global (base + row * row_bytes; rows past `last` repeat row `last`)
+// into the swizzled LDS tile `dst`. Lane i lands at position i % (D / 4) of row
+// kCopyRows j + i / (D / 4), so it loads logical chunk (i % (D / 4)) ^ f(row).
+template <int D>
+constexpr int kCopyRows = 256 / D;
+template <int D>
+__device__ __forceinline__ void copy_part(const float* base, unsigned row_bytes, int first_row,
+                                          int last_row, float* dst, int j, int lane) {
+  constexpr int kC = D / 4;
+  const int row = kCopyRows<D> * j + lane / kC;
+  const unsigned src_row = static_cast<unsigned>(min(first_row + row, last_row));
+  const unsigned c16 = 16u * static_cast<unsigned>(((lane % kC) ^ swz_f<D>(row)) & (kC - 1));
+  load_lds16(base, src_row * row_bytes + c16, dst + kCopyRows<D> * j * D);
 }
 
 // ---------------------------------------------------------------------------------------------
 // Forward. One workgroup = 4 waves x kFwdWaveQ queries of one (b, h) (QB in all); wave w owns
 // queries q0 + kFwdWaveQ w .., in kFwdNT column tiles of 16 (one query per lane column lo each).
 // Key tiles of KT keys are staged in LDS by direct copies (double buffered: the next tile's
-// copies in flight during this tile's math) and shared by the four waves. Two shapes are built
-// (measured on MI355X): non-causal QB 128 / KT 32 (each K / V operand read from LDS serves two
-// query tiles), causal QB 64 / KT 48 (smaller blocks balance the triangular work better).
-//   S^T = K Q^T per 16-key subtile and column tile n: A = K[key 16 mt + lo][dim 16 g + t] (LDS,
-//   float4 reads, shared by the column tiles), B = Q[query lo][dim 16 g + t] (registers, loaded
-//   once). Output: lane (lo, g) holds S[query lo][key 16 mt + 4 g + r].
-//   O^T += V^T P^T: M = dims (four 16-row tiles), N = queries, contraction over the tile's keys;
+// copies in flight during this tile's math) and shared by the four waves. The shapes per head_dim
+// and mask are in kFwdShape below (measured on MI355X for D 64: non-causal QB 128 / KT 32, each
+// K / V operand read from LDS serving two query tiles; causal QB 64 / KT 48, smaller blocks
+// balancing the triangular work).
+//   S^T = K Q^T per 16-key subtile and column tile n, D / 4 steps: A = K[key 16 mt + lo]
+//   [dim D/4 g + t] (LDS, float4 reads, shared by the column tiles), B = Q[query lo][dim D/4 g + t]
+//   (registers, loaded once). Output: lane (lo, g) holds S[query lo][key 16 mt + 4 g + r].
+//   O^T += V^T P^T: M = dims (D / 16 tiles of 16), N = queries, contraction over the tile's keys;
 //   step (kt, r) uses key 16 kt + 4 g + r, i.e. exactly the P value lane (lo, g) holds in its
 //   register (kt, r). A = V[key][dim 16 mt + lo] (LDS, shared by the column tiles).
 // Online softmax per query: running max m (identical in the four lanes of the query), running
@@ -179,18 +189,23 @@ struct FwdArgs {
   int causal;
 };
 
-template <int QB, int KT>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+template <int D, int QB, int KT, int WAVES>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)))
 fwd_kernel(FwdArgs a) {
   constexpr int kFwdQueries = QB;          // queries per workgroup
   constexpr int kFwdWaveQ = QB / 4;        // queries per wave
   constexpr int kFwdNT = kFwdWaveQ / 16;   // 16-query column tiles per wave
   constexpr int kFwdKeys = KT;             // keys per LDS tile
   constexpr int kFwdSub = KT / 16;         // 16-key subtiles per tile
-  __shared__ __attribute__((aligned(16))) float sK[2][kFwdKeys * kHeadDim];
-  __shared__ __attribute__((aligned(16))) float sV[2][kFwdKeys * kHeadDim];
+  constexpr int kQR = D / 4;               // Q values per lane and column tile
+  constexpr int kDT = D / 16;              // 16-dim tiles of O
+  constexpr int kCopies = KT / kCopyRows<D>;  // direct copies per K (or V) tile
+  static_assert(KT % kCopyRows<D> == 0, "whole copies per tile");
+  __shared__ __attribute__((aligned(16))) float sK[2][kFwdKeys * D];
+  __shared__ __attribute__((aligned(16))) float sV[2][kFwdKeys * D];
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lo = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, lo = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
   const int S = a.S, BH = a.B * a.H;
   int qb, bh;
   if (a.causal) {
@@ -212,15 +227,15 @@ fwd_kernel(FwdArgs a) {
   const unsigned k_ss4 = static_cast<unsigned>(a.k.ss) * 4u;
   const unsigned v_ss4 = static_cast<unsigned>(a.v.ss) * 4u;
 
-  // B operands of S^T: Q[qi(n)][16 g .. 16 g + 15] for this lane's query in column tile n.
-  float qr[kFwdNT][16];
+  // B operands of S^T: Q[qi(n)][D/4 g .. D/4 g + D/4 - 1] for this lane's query in column tile n.
+  float qr[kFwdNT][kQR];
 #pragma unroll
   for (int n = 0; n < kFwdNT; ++n) {
     const int qi = qw0 + 16 * n + lo;
     if (qi < S) {
-      const float* r = qp + qi * a.q.ss + 16 * g;
+      const float* r = qp + qi * a.q.ss + kQR * g;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kQR / 4; ++u) {
         const f4 x = ld4(r + 4 * u);
         qr[n][4 * u] = x.x;
         qr[n][4 * u + 1] = x.y;
@@ -229,7 +244,7 @@ fwd_kernel(FwdArgs a) {
       }
     } else {
 #pragma unroll
-      for (int t = 0; t < 16; ++t) qr[n][t] = 0.0f;
+      for (int t = 0; t < kQR; ++t) qr[n][t] = 0.0f;
     }
   }
 
@@ -239,21 +254,26 @@ fwd_kernel(FwdArgs a) {
   const int kw_end = a.causal ? min(S, qw0 + kFwdWaveQ) : S;
   const bool wave_live = qw0 < S;
 
-  // Staging: wave w copies K and V rows kFwdKeys / 4 * w .. + kFwdKeys / 4 - 1 of the tile; keys
-  // past S repeat key S - 1 (finite; their scores are masked, so 0 * V stays 0).
+  // Staging: wave w issues copies w, w + 4, ... of the K and V tiles; keys past S repeat key
+  // S - 1 (finite; their scores are masked, so 0 * V stays 0).
   auto stage = [&](int kt0, int buf) {
-    copy_rows<kFwdKeys / 16>(kp, k_ss4, kt0, S - 1, sK[buf], (kFwdKeys / 4) * w, lane);
-    copy_rows<kFwdKeys / 16>(vp, v_ss4, kt0, S - 1, sV[buf], (kFwdKeys / 4) * w, lane);
+#pragma unroll
+    for (int j0 = 0; j0 < kCopies; j0 += 4) {
+      if (j0 + w < kCopies) {
+        copy_part<D>(kp, k_ss4, kt0, S - 1, sK[buf], j0 + w, lane);
+        copy_part<D>(vp, v_ss4, kt0, S - 1, sV[buf], j0 + w, lane);
+      }
+    }
   };
 
-  f4 acc[kFwdNT][4];
+  f4 acc[kFwdNT][kDT];
   float m[kFwdNT], lsum[kFwdNT];
 #pragma unroll
   for (int n = 0; n < kFwdNT; ++n) {
     m[n] = kNegInf;
     lsum[n] = 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) acc[n][mt] = zero4();
+    for (int mt = 0; mt < kDT; ++mt) acc[n][mt] = zero4();
   }
 
   stage(0, 0);
@@ -278,8 +298,8 @@ fwd_kernel(FwdArgs a) {
         for (int n = 0; n < kFwdNT; ++n) s[n][mt] = zero4();
         if (live[mt]) {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const f4 kk = ld4(Kt + swz(16 * mt + lo, 16 * g + 4 * u));
+          for (int u = 0; u < kQR / 4; ++u) {
+            const f4 kk = ld4(Kt + swz<D>(16 * mt + lo, kQR * g + 4 * u));
 #pragma unroll
             for (int n = 0; n < kFwdNT; ++n) {
               s[n][mt] = mma(kk.x, qr[n][4 * u], s[n][mt]);
@@ -337,7 +357,7 @@ fwd_kernel(FwdArgs a) {
         lsum[n] = lsum[n] * alpha + psum;
         m[n] = m_new;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) acc[n][mt] *= alpha;
+        for (int mt = 0; mt < kDT; ++mt) acc[n][mt] *= alpha;
       }
 #pragma unroll
       for (int kt = 0; kt < kFwdSub; ++kt) {
@@ -345,8 +365,8 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            const float vv = Vt[swz(16 * kt + 4 * g + r, 16 * mt + lo)];
+          for (int mt = 0; mt < kDT; ++mt) {
+            const float vv = Vt[swz<D>(16 * kt + 4 * g + r, 16 * mt + lo)];
 #pragma unroll
             for (int n = 0; n < kFwdNT; ++n) acc[n][mt] = mma(vv, s[n][kt][r], acc[n][mt]);
           }
@@ -372,9 +392,9 @@ fwd_kernel(FwdArgs a) {
       const int qi = qw0 + 16 * n + lo;
       if (qi < S) {
         const float inv = 1.0f / l;
-        float* orow = a.o + ((static_cast<int64_t>(b) * S + qi) * a.H + h) * kHeadDim;
+        float* orow = a.o + ((static_cast<int64_t>(b) * S + qi) * a.H + h) * D;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) st4(orow + 16 * mt + 4 * g, acc[n][mt] * inv);
+        for (int mt = 0; mt < kDT; ++mt) st4(orow + 16 * mt + 4 * g, acc[n][mt] * inv);
         if (g == 0) a.lse[static_cast<int64_t>(bh) * S + qi] = m[n] + logf(l);
       }
     }
@@ -382,37 +402,37 @@ fwd_kernel(FwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward, step 1: D[b, h, i] = sum_c dO[b, i, h, c] O[b, i, h, c]. 16 lanes per row (one float4
-// each, then the xor butterfly 8, 4, 2, 1: one fixed order). It also clears the turn counters,
-// the ticket and the guard word of step 2 (stream order puts it first).
+// Backward, step 1: D[b, h, i] = sum_c dO[b, i, h, c] O[b, i, h, c]. D / 4 lanes per row (one
+// float4 each, then the xor butterfly D / 8, ..., 2, 1: one fixed order). It also clears the turn
+// counters, the ticket and the guard word of step 2 (stream order puts it first).
 // ---------------------------------------------------------------------------------------------
+template <int D>
 __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict__ o, View d_o,
                                                        float* __restrict__ dsum,
                                                        int* __restrict__ turn,
                                                        int* __restrict__ ctrl, int B, int H,
                                                        int S, int nturn) {
+  constexpr int kLanes = D / 4;  // lanes per row
   const int gtid = static_cast<int>(blockIdx.x) * kThreads + static_cast<int>(threadIdx.x);
   if (gtid < nturn) turn[gtid] = 0;
   if (gtid < 64) ctrl[gtid] = 0;
   const int64_t rows = static_cast<int64_t>(B) * H * S;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
-  const int c4 = threadIdx.x & 15;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / kLanes) + (threadIdx.x / kLanes);
+  const int c4 = threadIdx.x % kLanes;
   float x = 0.0f;
   if (row < rows) {
     const int i = static_cast<int>(row % S);
     const int64_t bh = row / S;
     const int h = static_cast<int>(bh % H), b = static_cast<int>(bh / H);
-    const f4 ov = ld4(o + ((static_cast<int64_t>(b) * S + i) * H + h) * kHeadDim + 4 * c4);
+    const f4 ov = ld4(o + ((static_cast<int64_t>(b) * S + i) * H + h) * D + 4 * c4);
     const f4 gv = ld4(d_o.p + b * d_o.sb + h * d_o.sh + i * d_o.ss + 4 * c4);
     x = ov.x * gv.x;
     x = fmaf(ov.y, gv.y, x);
     x = fmaf(ov.z, gv.z, x);
     x = fmaf(ov.w, gv.w, x);
   }
-  x += __shfl_xor(x, 8);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 1);
+#pragma unroll
+  for (int k = kLanes / 2; k >= 1; k /= 2) x += __shfl_xor(x, k);
   if (row < rows && c4 == 0) dsum[row] = x;
 }
 
@@ -424,15 +444,17 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
 // tiles of kQT = 16 (kNS = 1 subtile m of 16 queries; causal: from the block's first key on), the
 // next tile's Q, dO, L, D in flight during this one (LDS double buffer, filled by direct global ->
 // LDS copies).
-//   S = Q K^T and dP = dO V^T per subtile: M = queries, N = the wave's keys, contraction over d;
-//   A = Q / dO [query 16 m + lo][dim 16 g + t] (LDS, float4 reads), B = K / V [key lo][16 g + t].
+//   S = Q K^T and dP = dO V^T per subtile: M = queries, N = the wave's keys, contraction over the
+//   D dims in D / 4 steps: A = Q / dO [query 16 m + lo][dim D/4 g + t] (LDS, float4 reads),
+//   B = K / V [key lo][dim D/4 g + t].
 //   P = exp(S scale - L), dS = P o (dP - D), in place in the accumulators.
-//   dV^T += dO^T P, dK^T += Q^T dS: M = dims, N = keys, contraction over the tile's queries;
-//   step (m, r) uses query 16 m + 4 g + r: the P / dS value lane (lo, g) holds in register r of
-//   subtile m.
+//   dV^T += dO^T P, dK^T += Q^T dS: M = dims (D / 16 tiles), N = keys, contraction over the tile's
+//   queries; step (m, r) uses query 16 m + 4 g + r: the P / dS value lane (lo, g) holds in register
+//   r of subtile m.
 //   dQ partial = dS K over the block's 64 keys: dS goes through LDS (the one product that needs
-//   queries in lo); wave w computes dims 16 w .. + 15, step t contracting keys 16 g + t:
-//   A = dS[16 m + lo][16 g + t] (LDS, float4 reads), B = K[k0 + 16 g + t][16 w + lo] (registers).
+//   queries in lo); wave w computes the 16-dim tiles dt = w, w + 4, ... (< D / 16; at D 32 waves 2
+//   and 3 have none), step t contracting keys 16 g + t: A = dS[16 m + lo][16 g + t] (LDS, float4
+//   reads), B = K[k0 + 16 g + t][16 dt + lo] (registers).
 // split: the partial is stored to the key block's slot at the start of the next tile (plain
 // stores, nothing waits for them); step 3 (dq_kernel) sums the slots.
 // turns: the partial is added into dQ on the tile's turn, one tile later (software pipelined:
@@ -447,14 +469,14 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
 constexpr int kQT = kBwdQueryTile;
 constexpr int kNS = kQT / 16;  // 16-query subtiles per tile
 constexpr int kBwdLd = 68;     // dS tile pitch (floats): conflict-free reads and writes
-// Q and dO tiles are [kQT rows][64 floats] in the swizzled layout of swz(), filled by direct copies.
+// Q and dO tiles are [kQT rows][D floats] in the swizzled layout of swz(), filled by direct copies.
 
 struct BwdArgs {
   View q, k, v, d_o;
   const float* lse;
   const float* dsum;
   float* dqkv;
-  float* part;  // split: the dQ partials, [nkb][b h][ntile][kQT * 64] in fragment order
+  float* part;  // split: the dQ partials, [nkb][b h][ntile][kQT * D] in fragment order
   int* turn;
   int* ctrl;
   int B, H, S, nkb, ntile;
@@ -485,18 +507,9 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
 }
 __device__ __forceinline__ void wait_stores() { wait_mem(); }
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
-// Vector memory operations complete in issue order (vmcnt counts them down in order), so this
-// waits for everything but the last kStage1Loads operations issued: stage 1's loads.
-constexpr int kStage1Loads = 4 * kNS;
-static_assert(kStage1Loads == 4, "wait_except_stage1 encodes vmcnt(4)");
-__device__ __forceinline__ void wait_except_stage1() {
-  wait_vm<4>();
-}
-// split: everything but the partial's kNS stores, issued after the next tile's copies.
-static_assert(kNS == 1, "wait_except_part encodes vmcnt(1)");
-__device__ __forceinline__ void wait_except_part() {
-  wait_vm<1>();
-}
+// Vector memory operations complete in issue order (vmcnt counts them down in order), so
+// wait_vm<n> waits for everything but the last n operations issued: stage 1's loads (turns) or the
+// partial's stores (split), the last operations before a tile's first barrier.
 
 // Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised.
 __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
@@ -515,12 +528,20 @@ __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
 }
 
 // Occupancy target: BWD_WAVES waves per SIMD (the kernel is latency-bound: with fewer, the
-// matrix cores idle behind barriers and the dQ hand-over).
-template <bool kSplit>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BWD_WAVES)))
-bwd_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(16))) float sQ[2][kQT * kHeadDim];
-  __shared__ __attribute__((aligned(16))) float sdO[2][kQT * kHeadDim];
+// matrix cores idle behind barriers), 2 at D 128 (its registers do not fit 3).
+template <bool kSplit, int D>
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArgs a) {
+  constexpr int kKR = D / 4;                  // K (or V) values per lane: B operands of S, dP
+  constexpr int kDT = D / 16;                 // 16-dim tiles (dK, dV accumulators; dQ tiles)
+  constexpr int kDQ = (kDT + 3) / 4;          // dQ tiles per wave (w, w + 4, ...)
+  constexpr int kCopies = kQT / kCopyRows<D>;  // direct copies per Q (or dO) tile
+  // D 128: the dQ product's K comes from LDS (transposed, [D][kBwdLd]), its registers would not
+  // fit beside the others.
+  constexpr bool kKtLds = D == 128;
+  __shared__ __attribute__((aligned(16))) float sKt[kKtLds ? D * kBwdLd : 4];
+  __shared__ __attribute__((aligned(16))) float sQ[2][kQT * D];
+  __shared__ __attribute__((aligned(16))) float sdO[2][kQT * D];
   __shared__ __attribute__((aligned(16))) float sdS[kQT * kBwdLd];
   __shared__ __attribute__((aligned(16))) float sL[2][kQT];
   __shared__ __attribute__((aligned(16))) float sD[2][kQT];
@@ -561,6 +582,7 @@ bwd_kernel(BwdArgs a) {
   const int k0 = kb * kBwdKeys;
   const int kw0 = k0 + 16 * w;  // the wave's first key
   const int key = kw0 + lo;     // this lane's key
+  const bool wave_dq = w < kDT;  // the wave computes dQ tiles (all waves but 2, 3 at D 32)
   int* const guard = a.ctrl + kCtrlGuard;
 
   const float* qp = a.q.p + b * a.q.sb + h * a.q.sh;
@@ -573,21 +595,20 @@ bwd_kernel(BwdArgs a) {
   // Row strides in bytes (the host guarantees every offset within a (b, h) slice < 2^32).
   const unsigned q_ss4 = static_cast<unsigned>(a.q.ss) * 4u;
   const unsigned g_ss4 = static_cast<unsigned>(a.d_o.ss) * 4u;
-  // dQ of query qi, dims 16 w + lo: element dq_lane + qi * dq_row of dq_base (part 0 of the
-  // [b, s, 3, h, 64] gradient); the host guarantees s * 3 h * 64 < 2^32.
-  float* const dq_base = a.dqkv + static_cast<int64_t>(b) * S * 3 * a.H * kHeadDim +
-                         static_cast<int64_t>(h) * kHeadDim;
-  const unsigned dq_row = 3u * static_cast<unsigned>(a.H) * kHeadDim;
-  const unsigned dq_lane = 16u * w + lo;
+  // dQ of query qi, dim tile dt: element 16 dt + lo + qi * dq_row of dq_base (part 0 of the
+  // [b, s, 3, h, D] gradient); the host guarantees s * 3 h * D < 2^32.
+  float* const dq_base = a.dqkv + static_cast<int64_t>(b) * S * 3 * a.H * D +
+                         static_cast<int64_t>(h) * D;
+  const unsigned dq_row = 3u * static_cast<unsigned>(a.H) * D;
 
-  // B operands of S and dP: K[key][16 g .. 16 g + 15], V likewise; of the dQ product:
-  // kQ[t] = K[k0 + 16 g + t][16 w + lo]. Zero past S.
-  float kB[16], vB[16], kQ[16];
+  // B operands of S and dP: K[key][D/4 g .. D/4 g + D/4 - 1], V likewise; of the dQ product:
+  // kQ[j][t] = K[k0 + 16 g + t][16 (w + 4 j) + lo]. Zero past S.
+  float kB[kKR], vB[kKR], kQ[kKtLds ? 1 : kDQ][16];
   if (key < S) {
-    const float* kr = kp + key * a.k.ss + 16 * g;
-    const float* vr = vp + key * a.v.ss + 16 * g;
+    const float* kr = kp + key * a.k.ss + kKR * g;
+    const float* vr = vp + key * a.v.ss + kKR * g;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kKR / 4; ++u) {
       const f4 x = ld4(kr + 4 * u), y = ld4(vr + 4 * u);
       kB[4 * u] = x.x;
       kB[4 * u + 1] = x.y;
@@ -600,25 +621,43 @@ bwd_kernel(BwdArgs a) {
     }
   } else {
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
+    for (int t = 0; t < kKR; ++t) {
       kB[t] = 0.0f;
       vB[t] = 0.0f;
     }
   }
+  if constexpr (kKtLds) {
+    // sKt[dim][key] = K[k0 + key][dim] (zero past S); read after the first barrier below.
+    for (int i = tid; i < kBwdKeys * (D / 4); i += kThreads) {
+      const int kl = i / (D / 4), c = i % (D / 4), kk = k0 + kl;
+      const f4 x = kk < S ? ld4(kp + kk * a.k.ss + 4 * c) : zero4();
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    const int kk = k0 + 16 * g + t;
-    kQ[t] = kk < S ? kp[kk * a.k.ss + 16 * w + lo] : 0.0f;
+      for (int e = 0; e < 4; ++e) sKt[(4 * c + e) * kBwdLd + kl] = x[e];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kDQ; ++j) {
+      const int dt = w + 4 * j;
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int kk = k0 + 16 * g + t;
+        kQ[j][t] = kk < S && dt < kDT ? kp[kk * a.k.ss + 16 * dt + lo] : 0.0f;
+      }
+    }
   }
 
   // Staging of one query tile, all by direct copies (nothing passes through registers, so no
-  // wait is needed before the barrier that precedes the tile): wave w copies Q and dO rows
-  // kQT / 4 * w .. + kQT / 4 - 1, four rows per copy (lane i: row + i / 16, chunk position
-  // i % 16, i.e. logical chunk (i % 16) ^ row); wave 0 copies the tile's L, wave 1 its D (lanes
+  // wait is needed before the barrier that precedes the tile): wave w issues copies w, w + 4, ...
+  // of the Q and dO tiles (copy_part); wave 0 copies the tile's L, wave 1 its D (lanes
   // 0..kQT-1, one float each). Rows past S repeat row S - 1 (finite; masked later).
   auto gload = [&](int q0, int buf) {
-    copy_rows<kQT / 16>(qp, q_ss4, q0, S - 1, sQ[buf], (kQT / 4) * w, lane);
-    copy_rows<kQT / 16>(gp, g_ss4, q0, S - 1, sdO[buf], (kQT / 4) * w, lane);
+#pragma unroll
+    for (int j0 = 0; j0 < kCopies; j0 += 4) {
+      if (j0 + w < kCopies) {
+        copy_part<D>(qp, q_ss4, q0, S - 1, sQ[buf], j0 + w, lane);
+        copy_part<D>(gp, g_ss4, q0, S - 1, sdO[buf], j0 + w, lane);
+      }
+    }
     if (w < 2 && lane < kQT) {
       const unsigned off = 4u * static_cast<unsigned>(min(q0 + lane, S - 1));
       load_lds4(w == 0 ? lp : dp, off, w == 0 ? sL[buf] : sD[buf]);
@@ -649,9 +688,9 @@ bwd_kernel(BwdArgs a) {
     return a.causal ? min(a.nkb - 1, min(S - 1, j * kQT + kQT - 1) / kBwdKeys) + 1 : a.nkb;
   };
 
-  f4 dva[4], dka[4];
+  f4 dva[kDT], dka[kDT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < kDT; ++mt) {
     dva[mt] = zero4();
     dka[mt] = zero4();
   }
@@ -663,60 +702,76 @@ bwd_kernel(BwdArgs a) {
   // p1: partial computed, sums not yet loaded; p2: sums loaded, not yet stored. For each: the
   // tile's first query (-1: none), this block's position in the tile's order, the contributors.
   int p1_q0 = -1, p1_pos = 0, p1_cnt = 1, p2_q0 = -1, p2_pos = 0, p2_cnt = 1;
-  f4 p1[kNS], p2[kNS];
-  float p1s[kNS][4], p2s[kNS][4];
+  f4 p1[kDQ][kNS], p2[kDQ][kNS];
+  float p1s[kDQ][kNS][4], p2s[kDQ][kNS][4];
 #pragma unroll
-  for (int m = 0; m < kNS; ++m) {
-    p1[m] = zero4();
-    p2[m] = zero4();
+  for (int j = 0; j < kDQ; ++j) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p1s[m][r] = 0.0f;
-      p2s[m][r] = 0.0f;
+    for (int m = 0; m < kNS; ++m) {
+      p1[j][m] = zero4();
+      p2[j][m] = zero4();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p1s[j][m][r] = 0.0f;
+        p2s[j][m][r] = 0.0f;
+      }
     }
   }
-  // Stage 1 for the tile at q0p: this wave waits for the turn (one lane polls), then loads.
-  // Exactly kStage1Loads load instructions are issued (rows past S read row S - 1, unused), the
-  // last vector memory operations before the iteration's first barrier, so that barrier need not
-  // wait for them (see wait_except_stage1).
-  auto load_sums = [&](int q0p, int pos, int seen, float (&sums)[kNS][4]) {
-    if (pos == 0) return;
+  // Stage 1 for the tile at q0p (waves with dQ tiles): wait for the turn (one lane polls), then
+  // load. Exactly kStage1Loads load instructions are issued (rows past S read row S - 1, unused),
+  // the last vector memory operations before the iteration's first barrier, so that barrier need
+  // not wait for them.
+  constexpr int kStage1Loads = 4 * kNS * kDQ;
+  auto load_sums = [&](int q0p, int pos, int seen, float (&sums)[kDQ][kNS][4]) {
+    if (pos == 0 || !wave_dq) return;
     if (lane == 0 && seen != pos) wait_turn(tp + q0p / kQT, pos, guard);
     compiler_fence();
 #pragma unroll
-    for (int m = 0; m < kNS; ++m) {
+    for (int j = 0; j < kDQ; ++j) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int qi = min(q0p + 16 * m + 4 * g + r, S - 1);
-        sums[m][r] = ld_agent(dq_base + (dq_lane + qi * dq_row));
+      for (int m = 0; m < kNS; ++m) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qi = min(q0p + 16 * m + 4 * g + r, S - 1);
+          sums[j][m][r] = ld_agent(dq_base + (16u * (w + 4 * j) + lo + qi * dq_row));
+        }
       }
     }
     compiler_fence();
   };
   // Stage 2: the running sum plus this block's partial (x scale by the last contributor).
-  auto store_sums = [&](int q0p, int pos, int cnt, const f4 (&part)[kNS],
-                        const float (&sums)[kNS][4]) {
+  auto store_sums = [&](int q0p, int pos, int cnt, const f4 (&part)[kDQ][kNS],
+                        const float (&sums)[kDQ][kNS][4]) {
+    if (!wave_dq) return;
 #pragma unroll
-    for (int m = 0; m < kNS; ++m) {
+    for (int j = 0; j < kDQ; ++j) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int qi = q0p + 16 * m + 4 * g + r;
-        if (qi < S) {
-          float x = pos > 0 ? sums[m][r] + part[m][r] : part[m][r];
-          if (pos == cnt - 1) x *= a.scale;
-          st_agent(dq_base + (dq_lane + qi * dq_row), x);
+      for (int m = 0; m < kNS; ++m) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qi = q0p + 16 * m + 4 * g + r;
+          if (qi < S) {
+            float x = pos > 0 ? sums[j][m][r] + part[j][m][r] : part[j][m][r];
+            if (pos == cnt - 1) x *= a.scale;
+            st_agent(dq_base + (16u * (w + 4 * j) + lo + qi * dq_row), x);
+          }
         }
       }
     }
   };
   // split: this block's partial of the tile at q0p into its slot, in fragment order (register r
-  // of lane l of wave w, subtile m at m kQT 16 + w 256 + 4 l + r: one contiguous 1 KB store per
-  // wave and subtile).
-  auto store_part = [&](int q0p, const f4 (&part)[kNS]) {
+  // of lane l for dim tile dt of subtile m at (m kDT + dt) 256 + 4 l + r: one contiguous 1 KB
+  // store per dim tile and subtile).
+  constexpr int kPartStores = kNS * kDQ;
+  auto store_part = [&](int q0p, const f4 (&part)[kDQ][kNS]) {
+    if (!wave_dq) return;
     float* dst = a.part + ((static_cast<int64_t>(kb) * BH + bh) * a.ntile + q0p / kQT) *
-                              (kQT * kHeadDim) + 256 * w + 4 * lane;
+                              (kQT * D) + 4 * lane;
 #pragma unroll
-    for (int m = 0; m < kNS; ++m) st4(dst + m * (16 * kHeadDim), part[m]);
+    for (int j = 0; j < kDQ; ++j) {
+#pragma unroll
+      for (int m = 0; m < kNS; ++m) st4(dst + (m * kDT + w + 4 * j) * 256, part[j][m]);
+    }
   };
   // After stage 2's stores completed (vmcnt(0) and a barrier): the next contributor's turn.
   auto pass_turn = [&](int q0p, int pos, int cnt) {
@@ -746,7 +801,7 @@ bwd_kernel(BwdArgs a) {
     } else {
       // Stage 1's turn, read early (one lane, no wait here): by the time it is checked below the
       // value has arrived, and usually the turn with it.
-      if (p1_q0 >= 0 && p1_pos > 0 && lane == 0) {
+      if (p1_q0 >= 0 && p1_pos > 0 && wave_dq && lane == 0) {
         seen = __hip_atomic_load(tp + p1_q0 / kQT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       if (p2_q0 >= 0) store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);  // stage 2, two tiles back
@@ -769,8 +824,8 @@ bwd_kernel(BwdArgs a) {
       sP[m] = zero4();
       if (!live[m]) continue;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int at = swz(16 * m + lo, 16 * g + 4 * u);
+      for (int u = 0; u < kKR / 4; ++u) {
+        const int at = swz<D>(16 * m + lo, kKR * g + 4 * u);
         const f4 x = ld4(Qt + at), y = ld4(Gt + at);
         sS[m] = mma(x.x, kB[4 * u], sS[m]);
         sS[m] = mma(x.y, kB[4 * u + 1], sS[m]);
@@ -815,8 +870,8 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const int at = swz(16 * m + 4 * g + r, 16 * mt + lo);
+        for (int mt = 0; mt < kDT; ++mt) {
+          const int at = swz<D>(16 * m + 4 * g + r, 16 * mt + lo);
           dva[mt] = mma(Gt[at], sS[m][r], dva[mt]);
           dka[mt] = mma(Qt[at], sP[m][r], dka[mt]);
         }
@@ -831,8 +886,8 @@ bwd_kernel(BwdArgs a) {
     }
     if (kSplit) {
       // The next tile's copies complete (the partial's stores, issued after them, need not).
-      if (p1_q0 >= 0) {
-        wait_except_part();
+      if (p1_q0 >= 0 && wave_dq) {
+        wait_vm<kPartStores>();
       } else {
         wait_mem();
       }
@@ -840,8 +895,8 @@ bwd_kernel(BwdArgs a) {
     } else {
       // Stage 2's stores and the next tile's copies complete (stage 1's loads, issued last, may
       // still be in flight: they are needed only in the next iteration).
-      if (p1_q0 >= 0 && p1_pos > 0) {
-        wait_except_stage1();
+      if (p1_q0 >= 0 && p1_pos > 0 && wave_dq) {
+        wait_vm<kStage1Loads>();
       } else {
         wait_mem();
       }
@@ -853,24 +908,37 @@ bwd_kernel(BwdArgs a) {
       p2_pos = p1_pos;
       p2_cnt = p1_cnt;
 #pragma unroll
-      for (int m = 0; m < kNS; ++m) {
-        p2[m] = p1[m];
+      for (int j = 0; j < kDQ; ++j) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) p2s[m][r] = p1s[m][r];
+        for (int m = 0; m < kNS; ++m) {
+          p2[j][m] = p1[j][m];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) p2s[j][m][r] = p1s[j][m][r];
+        }
       }
     }
 #pragma unroll
     for (int m = 0; m < kNS; ++m) {
-      p1[m] = zero4();
-      if (q0 + 16 * m >= S) continue;
+#pragma unroll
+      for (int j = 0; j < kDQ; ++j) p1[j][m] = zero4();
+      if (q0 + 16 * m >= S || !wave_dq) continue;
       const float* sr = sdS + (16 * m + lo) * kBwdLd + 16 * g;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const f4 x = ld4(sr + 4 * u);
-        p1[m] = mma(x.x, kQ[4 * u], p1[m]);
-        p1[m] = mma(x.y, kQ[4 * u + 1], p1[m]);
-        p1[m] = mma(x.z, kQ[4 * u + 2], p1[m]);
-        p1[m] = mma(x.w, kQ[4 * u + 3], p1[m]);
+#pragma unroll
+        for (int j = 0; j < kDQ; ++j) {
+          f4 y;
+          if constexpr (kKtLds) {
+            y = ld4(&sKt[(16 * (w + 4 * j) + lo) * kBwdLd + 16 * g + 4 * u]);
+          } else {
+            y = f4{kQ[j][4 * u], kQ[j][4 * u + 1], kQ[j][4 * u + 2], kQ[j][4 * u + 3]};
+          }
+          p1[j][m] = mma(x.x, y.x, p1[j][m]);
+          p1[j][m] = mma(x.y, y.y, p1[j][m]);
+          p1[j][m] = mma(x.z, y.z, p1[j][m]);
+          p1[j][m] = mma(x.w, y.w, p1[j][m]);
+        }
       }
     }
     p1_q0 = q0;
@@ -906,11 +974,11 @@ bwd_kernel(BwdArgs a) {
 
   // dK (x scale) and dV of this lane's key: dims 16 mt + 4 g .. + 3, one float4 each.
   if (key < S) {
-    float* row = a.dqkv + (static_cast<int64_t>(b) * S + key) * 3 * a.H * kHeadDim +
-                 static_cast<int64_t>(h) * kHeadDim;
-    const int64_t part = static_cast<int64_t>(a.H) * kHeadDim;
+    float* row = a.dqkv + (static_cast<int64_t>(b) * S + key) * 3 * a.H * D +
+                 static_cast<int64_t>(h) * D;
+    const int64_t part = static_cast<int64_t>(a.H) * D;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < kDT; ++mt) {
       st4(row + part + 16 * mt + 4 * g, dka[mt] * a.scale);
       st4(row + 2 * part + 16 * mt + 4 * g, dva[mt]);
     }
@@ -920,80 +988,142 @@ bwd_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------------------------
 // Backward, step 3 (split only): dQ of one (b, h, query tile) per workgroup, the tile's partials
 // summed in key-block order, ((p_0 + p_1) + p_2) + ..., times scale (the same operations, in the
-// same order, as the turn hand-over). Thread i reads float4 i of each partial (fragment order:
-// lane l of wave w, registers r = 0..3 -> query 4 (l / 16) + r, dim 16 w + l % 16), then the tile
-// goes through LDS so that every row of dQ is written as 16 float4s.
+// same order, as the turn hand-over). Float4 i of a partial (fragment order: dim tile dt = i / 64
+// of subtile m, lane l = i % 64, registers r = 0..3 -> query 16 m + 4 (l / 16) + r, dim
+// 16 dt + l % 16) is summed by one thread, then the tile goes through LDS so that every row of dQ
+// is written as D / 4 float4s.
 // ---------------------------------------------------------------------------------------------
-static_assert(kQT * kHeadDim == 4 * kThreads, "dq_kernel: one float4 of the tile per thread");
-
+template <int D>
 __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ part,
                                                      float* __restrict__ dqkv, int B, int H,
                                                      int S, int nkb, int ntile, float scale,
                                                      int causal) {
-  __shared__ __attribute__((aligned(16))) float tile[kQT * kBwdLd];
+  constexpr int kDT = D / 16, kPitch = D + 4;  // pitch: conflict-free fragment writes
+  constexpr int kF4 = kQT * D / 4;             // float4s per tile
+  __shared__ __attribute__((aligned(16))) float tile[kQT * kPitch];
   const int tid = threadIdx.x;
   const int bh = static_cast<int>(blockIdx.x) / ntile, j = static_cast<int>(blockIdx.x) % ntile;
   const int b = bh / H, h = bh % H, q0 = j * kQT;
   // Contributors: causal, the key blocks holding a key <= the tile's last query.
   const int cnt = causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) + 1 : nkb;
-  const int64_t slot = static_cast<int64_t>(B) * H * ntile * (kQT * kHeadDim);
-  const float* src = part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * kHeadDim) + 4 * tid;
-  f4 acc = ld4(src);
-  for (int kb = 1; kb < cnt; ++kb) acc += ld4(src + kb * slot);
-  acc *= scale;
-  const int w = tid >> 6, lane = tid & 63, lo = lane & 15, g = lane >> 4;
+  const int64_t slot = static_cast<int64_t>(B) * H * ntile * (kQT * D);
+  const float* src = part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) tile[(4 * g + r) * kBwdLd + 16 * w + lo] = acc[r];
+  for (int i = tid; i < kF4; i += kThreads) {
+    f4 acc = ld4(src + 4 * i);
+    for (int kb = 1; kb < cnt; ++kb) acc += ld4(src + kb * slot + 4 * i);
+    acc *= scale;
+    const int lane = i & 63, md = i >> 6, dt = md % kDT, m = md / kDT;
+    const int lo = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tile[(16 * m + 4 * g + r) * kPitch + 16 * dt + lo] = acc[r];
+  }
   __syncthreads();
-  const int row = tid >> 4, c4 = tid & 15;
-  if (q0 + row < S) {
-    st4(dqkv + (static_cast<int64_t>(b) * S + q0 + row) * 3 * H * kHeadDim +
-            static_cast<int64_t>(h) * kHeadDim + 4 * c4,
-        ld4(&tile[row * kBwdLd + 4 * c4]));
+#pragma unroll
+  for (int i = tid; i < kF4; i += kThreads) {
+    const int row = i / (D / 4), c4 = i % (D / 4);
+    if (q0 + row < S) {
+      st4(dqkv + (static_cast<int64_t>(b) * S + q0 + row) * 3 * H * D +
+              static_cast<int64_t>(h) * D + 4 * c4,
+          ld4(&tile[row * kPitch + 4 * c4]));
+    }
   }
 }
 
 }  // namespace
 
-// The two forward shapes: queries per workgroup, keys per tile.
-constexpr int kFwdQB[2] = {128, 64};  // [causal]
-constexpr int kFwdKT[2] = {32, 48};
+// Forward shapes per head_dim and mask: queries per workgroup, keys per tile, waves per SIMD
+// (D 128: two, its K / V tiles take 64 KB of LDS per workgroup).
+template <int D, int C>
+struct FwdCfg;
+template <>
+struct FwdCfg<32, 0> {
+  static constexpr int QB = 128, KT = 64, W = 3;
+};
+template <>
+struct FwdCfg<32, 1> {
+  static constexpr int QB = 64, KT = 32, W = 3;
+};
+template <>
+struct FwdCfg<64, 0> {
+  static constexpr int QB = 128, KT = 32, W = 3;
+};
+template <>
+struct FwdCfg<64, 1> {
+  static constexpr int QB = 64, KT = 48, W = 3;
+};
+template <>
+struct FwdCfg<128, 0> {
+  static constexpr int QB = 64, KT = 32, W = 2;
+};
+template <>
+struct FwdCfg<128, 1> {
+  static constexpr int QB = 64, KT = 32, W = 2;
+};
 
-int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal) {
-  const int qb = kFwdQB[causal ? 1 : 0];
+namespace {
+
+template <int D, int C>
+const void* fwd_fn() {
+  using F = FwdCfg<D, C>;
+  return reinterpret_cast<const void*>(fwd_kernel<D, F::QB, F::KT, F::W>);
+}
+
+int fwd_qb(int d, int causal) {
+  const int c = causal ? 1 : 0;
+  switch (d) {
+    case 32: return c ? FwdCfg<32, 1>::QB : FwdCfg<32, 0>::QB;
+    case 128: return c ? FwdCfg<128, 1>::QB : FwdCfg<128, 0>::QB;
+    default: return c ? FwdCfg<64, 1>::QB : FwdCfg<64, 0>::QB;
+  }
+}
+
+hipError_t launch(const void* fn, int64_t blocks, void** args, void* stream) {
+  return hipLaunchKernel(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), args, 0,
+                         static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+bool head_dim_supported(int64_t d) { return d == 32 || d == 64 || d == 128; }
+
+int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal, int d) {
+  const int qb = fwd_qb(d, causal);
   return ((s + qb - 1) / qb) * h * b;
 }
 int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s) {
   return ((s + kBwdKeys - 1) / kBwdKeys) * h * b;
 }
-int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s) { return (b * h * s + 15) / 16; }
+int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d) {
+  const int64_t rows_per_block = kThreads / (d / 4);
+  return (b * h * s + rows_per_block - 1) / rows_per_block;
+}
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQT - 1) / kQT); }
 
-int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s,
+int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s, int d,
                    float scale, int causal, void* stream) {
   const int c = causal ? 1 : 0;
-  FwdArgs a{q, k, v, o, lse, b, h, s, (s + kFwdQB[c] - 1) / kFwdQB[c], scale, c};
+  const int qb = fwd_qb(d, c);
+  FwdArgs a{q, k, v, o, lse, b, h, s, (s + qb - 1) / qb, scale, c};
   void* args[] = {&a};
-  const void* fn = c ? reinterpret_cast<const void*>(fwd_kernel<kFwdQB[1], kFwdKT[1]>)
-                     : reinterpret_cast<const void*>(fwd_kernel<kFwdQB[0], kFwdKT[0]>);
-  return static_cast<int>(hipLaunchKernel(fn,
-                                          dim3(static_cast<unsigned>(forward_blocks(b, h, s, c))),
-                                          dim3(kThreads), args, 0,
-                                          static_cast<hipStream_t>(stream)));
+  const void* fn = d == 32    ? (c ? fwd_fn<32, 1>() : fwd_fn<32, 0>())
+                   : d == 128 ? (c ? fwd_fn<128, 1>() : fwd_fn<128, 0>())
+                              : (c ? fwd_fn<64, 1>() : fwd_fn<64, 0>());
+  return static_cast<int>(launch(fn, forward_blocks(b, h, s, c, d), args, stream));
 }
 
 int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl, int b, int h,
-                    int s, void* stream) {
+                    int s, int d, void* stream) {
   int nturn = b * h * ((s + kQT - 1) / kQT);
   void* args[] = {&o, &d_o, &dsum, &turn, &ctrl, &b, &h, &s, &nturn};
-  return static_cast<int>(hipLaunchKernel(reinterpret_cast<const void*>(prep_kernel),
-                                          dim3(static_cast<unsigned>(bwd_prep_blocks(b, h, s))),
-                                          dim3(kThreads), args, 0,
-                                          static_cast<hipStream_t>(stream)));
+  const void* fn = d == 32    ? reinterpret_cast<const void*>(prep_kernel<32>)
+                   : d == 128 ? reinterpret_cast<const void*>(prep_kernel<128>)
+                              : reinterpret_cast<const void*>(prep_kernel<64>);
+  return static_cast<int>(launch(fn, bwd_prep_blocks(b, h, s, d), args, stream));
 }
 
 int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
-                    float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s,
+                    float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s, int d,
                     float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
   const bool split = part != nullptr;
@@ -1001,22 +1131,28 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const fl
   BwdArgs a{q, k, v, d_o, lse, dsum, dqkv, part, turn, ctrl, b, h, s,
             nkb, ntile, scale, causal, stagger};
   void* args[] = {&a};
-  const void* fn = split ? reinterpret_cast<const void*>(bwd_kernel<true>)
-                         : reinterpret_cast<const void*>(bwd_kernel<false>);
-  return static_cast<int>(hipLaunchKernel(fn,
-                                          dim3(static_cast<unsigned>(bwd_main_blocks(b, h, s))),
-                                          dim3(kThreads), args, 0,
-                                          static_cast<hipStream_t>(stream)));
+  const void* fn;
+  if (d == 32) {
+    fn = split ? reinterpret_cast<const void*>(bwd_kernel<true, 32>)
+               : reinterpret_cast<const void*>(bwd_kernel<false, 32>);
+  } else if (d == 128) {
+    fn = split ? reinterpret_cast<const void*>(bwd_kernel<true, 128>)
+               : reinterpret_cast<const void*>(bwd_kernel<false, 128>);
+  } else {
+    fn = split ? reinterpret_cast<const void*>(bwd_kernel<true, 64>)
+               : reinterpret_cast<const void*>(bwd_kernel<false, 64>);
+  }
+  return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
 }
 
-int launch_bwd_dq(const float* part, float* dqkv, int b, int h, int s, float scale, int causal,
-                  void* stream) {
+int launch_bwd_dq(const float* part, float* dqkv, int b, int h, int s, int d, float scale,
+                  int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
   void* args[] = {&part, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
-  return static_cast<int>(hipLaunchKernel(reinterpret_cast<const void*>(dq_kernel),
-                                          dim3(static_cast<unsigned>(bwd_dq_blocks(b, h, s))),
-                                          dim3(kThreads), args, 0,
-                                          static_cast<hipStream_t>(stream)));
+  const void* fn = d == 32    ? reinterpret_cast<const void*>(dq_kernel<32>)
+                   : d == 128 ? reinterpret_cast<const void*>(dq_kernel<128>)
+                              : reinterpret_cast<const void*>(dq_kernel<64>);
+  return static_cast<int>(launch(fn, bwd_dq_blocks(b, h, s), args, stream));
 }
 
 }  // namespace fattn

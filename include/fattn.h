@@ -1,14 +1,17 @@
 /*
  * fattn.h -- the C ABI of the MI355X (gfx950) fused fp32 scaled-dot-product attention,
- * head_dim 64, forward and deterministic backward.
+ * forward and deterministic backward, head_dim 32, 64 or 128.
  *
  * This is the drop-in boundary for the reference crate's hot path
- * (mi-for-the-rust-of-us/candle-fused-attn v0.4.0). Each entry point names the reference
- * interface it replaces (path:line in that crate). Two levels are exported:
+ * (mi-for-the-rust-of-us/candle-fused-attn v0.4.0), whose kernels take head_dim 64 (32 and 128
+ * are on its roadmap, ROADMAP.md:76-79). Each entry point names the reference interface it
+ * replaces (path:line in that crate). Two levels are exported:
  *
  *   - kernel level (replaces the launcher src/cuda.rs and the three kernels of
- *     kernels/fused_attn.cu): operands are [b, h, s, 64] views given by a base pointer (the
- *     view's first element) and (batch, head, seq) strides in floats, head_dim contiguous;
+ *     kernels/fused_attn.cu): operands are [b, h, s, d] views given by a base pointer (the
+ *     view's first element) and (batch, head, seq) strides in floats, head_dim contiguous. The
+ *     `fattn_*_f32` entries take any supported d; the `fattn_*_f32_d64` entries, named after the
+ *     reference's kernels, are the same with the reference's check (d must be 64);
  *   - op level (replaces the candle custom ops' device bodies in src/lib.rs): operands are given
  *     as a storage pointer, an element offset, a shape and strides, exactly what a candle
  *     `Layout` holds, and the geometry, shape and alignment checks of src/lib.rs run here.
@@ -37,12 +40,15 @@
 extern "C" {
 #endif
 
-/* The one head dimension the kernels are built for (src/lib.rs:91, CUDA_HEAD_DIM). */
+/* The reference's head dimension (src/lib.rs:91, CUDA_HEAD_DIM); the kernels here are also
+ * built for FATTN_HEAD_DIM_MIN (32) and FATTN_HEAD_DIM_MAX (128). */
 #define FATTN_HEAD_DIM 64
+#define FATTN_HEAD_DIM_MIN 32
+#define FATTN_HEAD_DIM_MAX 128
 
 /* Validation failures (negative return codes). */
 #define FATTN_EINVAL (-1)     /* null pointer, bad rank/shape, non-contiguous last dim, ... */
-#define FATTN_EHEADDIM (-2)   /* head_dim != 64 (src/cuda.rs:85-93) */
+#define FATTN_EHEADDIM (-2)   /* head_dim not built (src/cuda.rs:85-93: the reference's is 64) */
 #define FATTN_EALIGN (-3)     /* a row is not 16-byte aligned (src/lib.rs:431-435, :533-538) */
 #define FATTN_ERANGE (-4)     /* a size exceeds the kernels' index or grid range */
 #define FATTN_EWORKSPACE (-5) /* workspace missing, too small or misaligned */
@@ -53,53 +59,77 @@ extern "C" {
  * fattn_bwd_f32_d64 (:213-426). Strides are {batch, head, seq} in floats.
  * ------------------------------------------------------------------------------------------ */
 
-/* Forward: O [b, s, h, 64] contiguous (the merge-heads layout) and L [b, h, s], the row
+/* Forward: O [b, s, h, d] contiguous (the merge-heads layout) and L [b, h, s], the row
  * log-sum-exp the backward needs. Replaces cuda::forward (src/cuda.rs:139-185). */
-int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,
-                      int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
-                      const int64_t q_strides[3], const int64_t k_strides[3],
-                      const int64_t v_strides[3], void* stream);
+int fattn_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse,
+                  int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
+                  const int64_t q_strides[3], const int64_t k_strides[3],
+                  const int64_t v_strides[3], void* stream);
 
 /* Backward workspace (256-byte aligned). Replaces the temporaries cuda::backward allocates
  * (dsum and turn, src/cuda.rs:200-209). Its size picks how dQ is summed over key blocks:
  *   >= fattn_bwd_workspace_split_bytes: "split" -- every key block writes its dQ partials to the
- *      workspace (about 4 * s * s * b * h bytes) and a third kernel sums them in key-block order;
- *      no workgroup waits on another (the faster way);
+ *      workspace (about s * s * b * h * d / 16 bytes) and a third kernel sums them in key-block
+ *      order; no workgroup waits on another (the faster way);
  *   >= fattn_bwd_workspace_min_bytes (below split): "turns" -- key blocks add into dQ in place,
  *      in key-block order, under per-query-tile turn counters; D, counters and ticket only.
  * Both are deterministic. fattn_bwd_workspace_bytes is the split size when that is at most
- * FATTN_SPLIT_MAX_BYTES, else the minimum. */
+ * FATTN_SPLIT_MAX_BYTES, else the minimum. All three return 0 for a negative size or an
+ * unsupported d. */
 #define FATTN_SPLIT_MAX_BYTES ((size_t)4 << 30)
-size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s);
-size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s);
-size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s);
+size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s, int64_t d);
+size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s, int64_t d);
+size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s, int64_t d);
 
 /* Backward step 1: D[b, h, i] = sum_c dO[b, i, h, c] * O[b, i, h, c] (fixed order) and the
- * counters of step 2 cleared. O is [b, s, h, 64] contiguous; dO is read through do_strides.
+ * counters of step 2 cleared. O is [b, s, h, d] contiguous; dO is read through do_strides.
  * Replaces the fattn_bwd_dot_f32_d64 launch (src/cuda.rs:215-231). */
-int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_strides[3],
-                           void* workspace, size_t workspace_bytes,
-                           int64_t b, int64_t h, int64_t s, int64_t d, void* stream);
+int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_strides[3],
+                       void* workspace, size_t workspace_bytes, int64_t b, int64_t h, int64_t s,
+                       int64_t d, void* stream);
 
-/* Backward step 2: dK and dV into ONE [b, s, 3, h, 64] buffer (the fused qkv projection's
+/* Backward step 2: dK and dV into ONE [b, s, 3, h, d] buffer (the fused qkv projection's
  * gradient layout); dQ summed over key blocks in a fixed order, so every rerun is bit-identical:
  * with a split-size workspace its partials go to the workspace (step 3 finishes dQ), else dQ is
  * complete after this step. Needs step 1 on the same workspace first. Replaces the
  * fattn_bwd_f32_d64 launch (src/cuda.rs:233-258). */
+int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* d_o,
+                       const float* lse, float* dqkv, void* workspace, size_t workspace_bytes,
+                       int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
+                       const int64_t q_strides[3], const int64_t k_strides[3],
+                       const int64_t v_strides[3], const int64_t do_strides[3], void* stream);
+
+/* Backward step 3: with a split-size workspace, dQ = scale * (sum of step 2's partials in
+ * key-block order) into part 0 of dqkv; with a smaller one nothing to do (returns 0). Has no
+ * counterpart launch in the reference (its dQ is summed in place, as the turn mode here). */
+int fattn_bwd_dq_f32(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
+                     int64_t s, int64_t d, float scale, int causal, void* stream);
+
+/* All backward steps. Replaces cuda::backward (src/cuda.rs:187-260). */
+int fattn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
+                  const float* d_o, const float* lse, float* dqkv, void* workspace,
+                  size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                  float scale, int causal, const int64_t q_strides[3],
+                  const int64_t k_strides[3], const int64_t v_strides[3],
+                  const int64_t do_strides[3], void* stream);
+
+/* The same five under the reference's kernel names, with its head_dim check (d must be 64,
+ * else FATTN_EHEADDIM with the reference's message, src/cuda.rs:85-93). */
+int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,
+                      int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
+                      const int64_t q_strides[3], const int64_t k_strides[3],
+                      const int64_t v_strides[3], void* stream);
+int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_strides[3],
+                           void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
+                           int64_t s, int64_t d, void* stream);
 int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
                            const float* lse, float* dqkv, void* workspace,
                            size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
                            float scale, int causal, const int64_t q_strides[3],
                            const int64_t k_strides[3], const int64_t v_strides[3],
                            const int64_t do_strides[3], void* stream);
-
-/* Backward step 3: with a split-size workspace, dQ = scale * (sum of step 2's partials in
- * key-block order) into part 0 of dqkv; with a smaller one nothing to do (returns 0). Has no
- * counterpart launch in the reference (its dQ is summed in place, as the turn mode here). */
 int fattn_bwd_dq_f32_d64(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b,
                          int64_t h, int64_t s, int64_t d, float scale, int causal, void* stream);
-
-/* All backward steps. Replaces cuda::backward (src/cuda.rs:187-260). */
 int fattn_bwd_f32_d64(const float* q, const float* k, const float* v, const float* o,
                       const float* d_o, const float* lse, float* dqkv, void* workspace,
                       size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
@@ -164,7 +194,7 @@ const char* fattn_version(void);
 
 /* Synchronises `stream`, then reads the backward's guard word from `workspace` into *status:
  * 0 = every dQ turn wait ended normally; nonzero = some wait hit its spin bound (the turn
- * protocol failed, results are invalid). For tests and debugging. */
+ * protocol failed, results are invalid). For tests and debugging; any head_dim. */
 int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                      int64_t s, void* stream, int* status);
 

@@ -46,20 +46,26 @@ def a3(*x):
 
 def test_workspace_size_is_aligned_and_monotone():
     L = _lib.lib()
-    n1 = L.fattn_bwd_workspace_bytes(64, 6, 240)
-    lo, hi = L.fattn_bwd_workspace_min_bytes(64, 6, 240), L.fattn_bwd_workspace_split_bytes(64, 6, 240)
+    n1 = L.fattn_bwd_workspace_bytes(64, 6, 240, 64)
+    lo = L.fattn_bwd_workspace_min_bytes(64, 6, 240, 64)
+    hi = L.fattn_bwd_workspace_split_bytes(64, 6, 240, 64)
     assert n1 % 256 == 0 and lo % 256 == 0 and hi % 256 == 0
     # minimum: D (64*6*240 f32) + turns (64*6*15 i32) + control
     assert lo >= 64 * 6 * 240 * 4 + 64 * 6 * 15 * 4 + 256
-    # split: plus one 16 x 64 f32 partial per key block (4) and query tile (15) of each (b, h)
+    # split: plus one 16 x d f32 partial per key block (4) and query tile (15) of each (b, h)
     assert hi == lo + 4 * 64 * 6 * 15 * 16 * 64 * 4
     assert n1 == hi  # 94 MB: below the split cap
-    assert L.fattn_bwd_workspace_bytes(64, 6, 241) >= n1
-    assert L.fattn_bwd_workspace_bytes(-1, 6, 240) == 0
-    assert L.fattn_bwd_workspace_min_bytes(-1, 6, 240) == 0
+    for d in (32, 128):
+        assert L.fattn_bwd_workspace_min_bytes(64, 6, 240, d) == lo
+        assert L.fattn_bwd_workspace_split_bytes(64, 6, 240, d) == lo + 4 * 64 * 6 * 15 * 16 * d * 4
+    assert L.fattn_bwd_workspace_bytes(64, 6, 241, 64) >= n1
+    assert L.fattn_bwd_workspace_bytes(-1, 6, 240, 64) == 0
+    assert L.fattn_bwd_workspace_min_bytes(-1, 6, 240, 64) == 0
+    assert L.fattn_bwd_workspace_bytes(64, 6, 240, 48) == 0      # head_dim not built
     # Past FATTN_SPLIT_MAX_BYTES (4 GiB) the default falls back to the minimum (turns).
-    assert L.fattn_bwd_workspace_split_bytes(1, 64, 16384) > 4 << 30
-    assert L.fattn_bwd_workspace_bytes(1, 64, 16384) == L.fattn_bwd_workspace_min_bytes(1, 64, 16384)
+    assert L.fattn_bwd_workspace_split_bytes(1, 64, 16384, 64) > 4 << 30
+    assert (L.fattn_bwd_workspace_bytes(1, 64, 16384, 64)
+            == L.fattn_bwd_workspace_min_bytes(1, 64, 16384, 64))
 
 
 def test_head_dim_gate_before_alignment():
@@ -69,10 +75,19 @@ def test_head_dim_gate_before_alignment():
     rc = L.fattn_qkv_forward(BAD, 1, a3(2, 5, 3 * 4 * 6), a3(5 * 72, 72, 1), 4, 0.3, 0, BAD,
                              BAD, None)
     assert rc == _lib.FATTN_EHEADDIM
-    assert "head_dim 64, got 6" in _lib.last_error()
+    assert "head_dim 32, 64 or 128, got 6" in _lib.last_error()
     assert _lib.last_error().startswith("fused_attention")
+    # The reference-named kernel-level entries keep its check (head_dim 64 only); the generic
+    # ones take 32, 64, 128.
     rc = L.fattn_fwd_f32_d64(BAD, BAD, BAD, BAD, BAD, 1, 1, 8, 32, 0.1, 0, st, st, st, None)
     assert rc == _lib.FATTN_EHEADDIM
+    assert "head_dim 64, got 32" in _lib.last_error()
+    rc = L.fattn_fwd_f32(BAD, BAD, BAD, BAD, BAD, 1, 1, 8, 96, 0.1, 0, st, st, st, None)
+    assert rc == _lib.FATTN_EHEADDIM
+    assert "head_dim 32, 64 or 128, got 96" in _lib.last_error()
+    ok = a3(8 * 32, 32, 32)
+    rc = L.fattn_fwd_f32(ODD, BAD, BAD, BAD, BAD, 1, 1, 8, 32, 0.1, 0, ok, ok, ok, None)
+    assert rc == _lib.FATTN_EALIGN   # past the head_dim gate: the misaligned pointer
 
 
 def test_qkv_geometry_errors():
@@ -117,8 +132,8 @@ def test_general_path_errors():
     rc = L.fattn_forward(BAD, 2, sh, st, BAD, 0, sh, st, BAD, 0, sh, st, 0.1, 0, BAD, BAD, None)
     assert rc == _lib.FATTN_EALIGN
     assert _lib.last_error() == "fused_attention: rows must be 16-byte aligned"
-    sh32 = a3(2, 3, 5, 32)
-    rc = L.fattn_forward(BAD, 0, sh32, st, BAD, 0, sh32, st, BAD, 0, sh32, st, 0.1, 0, BAD,
+    sh48 = a3(2, 3, 5, 48)   # a head_dim the kernels are not built for
+    rc = L.fattn_forward(BAD, 0, sh48, st, BAD, 0, sh48, st, BAD, 0, sh48, st, 0.1, 0, BAD,
                          BAD, None)
     assert rc == _lib.FATTN_EHEADDIM
 
@@ -178,7 +193,7 @@ def test_range_limits():
     assert rc == _lib.FATTN_ERANGE
     assert "exceeds" in _lib.last_error()
     # 65,536 batches (the reference's gridDim.z limit) is fine here: the grid is one-dimensional
-    ws = L.fattn_bwd_workspace_bytes(65536, 1, 1)
+    ws = L.fattn_bwd_workspace_bytes(65536, 1, 1, 64)
     assert ws > 0
 
 
@@ -204,7 +219,7 @@ def test_alignment_predicates():
     assert cfa.float4_aligned(buf.transpose(1, 2))       # config 5's views are read in place
     odd = torch.zeros(2, 3, 5, 66)[..., :64]
     assert cfa.float4_aligned(odd) is False              # seq stride 66 is not a multiple of 4
-    assert cfa.CUDA_HEAD_DIM == 64
+    assert cfa.CUDA_HEAD_DIM == 64 and cfa.HIP_HEAD_DIMS == (32, 64, 128)
 
 
 def test_slice_offsets_must_fit_32_bits():
