@@ -222,8 +222,8 @@ def main() -> int:
                        "step": round(steps_us, 2)},
         "dq_sum": "split" if split else "turns",
         "roofline": {
-            "kernel": ("bwd_kernel<true> (fattn_bwd_main_f32_d64, split)" if split
-                       else "bwd_kernel<false> (fattn_bwd_main_f32_d64, turns)"),
+            "kernel": ("bwd_kernel<true, 64> (fattn_bwd_main_f32_d64, split)" if split
+                       else "bwd_kernel<false, 64> (fattn_bwd_main_f32_d64, turns)"),
             "bound": "mfma",
             "achieved": round(main_tflops, 3),
             "peak": PEAK_FP32_MFMA_TFLOPS,
