@@ -53,6 +53,9 @@ struct Var {
 constexpr int kThreads = 256;  // 4 waves of 64
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kNegInf = -__builtin_inff();
+// Forward lazy rescaling: a row's reference max moves only when a tile's max exceeds it by more
+// than this many powers of two (unnormalised probabilities stay below 2^8).
+constexpr float kRescaleLog2 = 8.0f;
 // A dQ turn wait gives up after this many polls (about a second) and raises the guard word,
 // so a protocol failure ends the kernel instead of hanging the GPU.
 constexpr int kSpinBound = 1 << 20;
@@ -175,9 +178,12 @@ __device__ __forceinline__ void copy_part(const float* base, unsigned row_bytes,
 //   O^T += V^T P^T: M = dims (D / 16 tiles of 16), N = queries, contraction over the tile's keys;
 //   step (kt, r) uses key 16 kt + 4 g + r, i.e. exactly the P value lane (lo, g) holds in its
 //   register (kt, r). A = V[key][dim 16 mt + lo] (LDS, shared by the column tiles).
-// Online softmax per query: running max m (identical in the four lanes of the query), running
-// partial sum over the lane's own keys (combined across the four lanes once, in a fixed order,
-// at the end), O rescaled by alpha = exp(m_old - m_new) when the max grows.
+// Online softmax per query, in the log2 domain on raw scores: p = 2^(s c2 - m c2), c2 = |scale|
+// log2 e (q negated for a negative scale), one fma and one exp per score. m is a reference max
+// (identical in the four lanes of the query) that moves only when a tile's max exceeds it by more
+// than 2^kRescaleLog2, O and the row sum being rescaled then (lazily: most tiles skip it); the row
+// sum is a partial sum over the lane's own keys, combined across the four lanes once, in a fixed
+// order, at the end. L = m |scale| + ln(sum).
 // ---------------------------------------------------------------------------------------------
 
 struct FwdArgs {
@@ -227,7 +233,9 @@ fwd_kernel(FwdArgs a) {
   const unsigned k_ss4 = static_cast<unsigned>(a.k.ss) * 4u;
   const unsigned v_ss4 = static_cast<unsigned>(a.v.ss) * 4u;
 
-  // B operands of S^T: Q[qi(n)][D/4 g .. D/4 g + D/4 - 1] for this lane's query in column tile n.
+  // B operands of S^T: Q[qi(n)][D/4 g .. D/4 g + D/4 - 1] for this lane's query in column tile n,
+  // negated for a negative scale (so that the raw scores' max is the scaled scores' max).
+  const float qsign = a.scale < 0.0f ? -1.0f : 1.0f;
   float qr[kFwdNT][kQR];
 #pragma unroll
   for (int n = 0; n < kFwdNT; ++n) {
@@ -236,7 +244,7 @@ fwd_kernel(FwdArgs a) {
       const float* r = qp + qi * a.q.ss + kQR * g;
 #pragma unroll
       for (int u = 0; u < kQR / 4; ++u) {
-        const f4 x = ld4(r + 4 * u);
+        const f4 x = ld4(r + 4 * u) * qsign;
         qr[n][4 * u] = x.x;
         qr[n][4 * u + 1] = x.y;
         qr[n][4 * u + 2] = x.z;
@@ -247,6 +255,9 @@ fwd_kernel(FwdArgs a) {
       for (int t = 0; t < kQR; ++t) qr[n][t] = 0.0f;
     }
   }
+
+  // Scores enter the exponent as s * c2 (c2 = |scale| log2 e); m holds raw-score maxima.
+  const float ascale = fabsf(a.scale), c2 = ascale * kLog2e;
 
   // Keys the block needs, and keys this wave's rows can see.
   const int k_end = a.causal ? min(S, q0 + kFwdQueries) : S;
@@ -313,18 +324,15 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int n = 0; n < kFwdNT; ++n) {
         const int qi = qw0 + 16 * n + lo;
-        // Scale, mask (keys past S; causal keys after the query), tile max. Non-causal tiles
-        // whose keys are all below S (wave-uniform test) skip the mask.
+        // Mask (keys past S; causal keys after the query) and the tile's row max of the raw
+        // scores. Non-causal tiles whose keys are all below S (wave-uniform test) skip the mask.
         float tmax = kNegInf;
-        if (!a.causal && kt0 + kFwdKeys <= S) {
+        const bool full = !a.causal && kt0 + kFwdKeys <= S;
+        if (full) {
 #pragma unroll
           for (int mt = 0; mt < kFwdSub; ++mt) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float x = s[n][mt][r] * a.scale;
-              s[n][mt][r] = x;
-              tmax = fmaxf(tmax, x);
-            }
+            for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, s[n][mt][r]);
           }
         } else {
 #pragma unroll
@@ -333,31 +341,54 @@ fwd_kernel(FwdArgs a) {
             for (int r = 0; r < 4; ++r) {
               const int key = kt0 + 16 * mt + 4 * g + r;
               const bool ok = live[mt] && key < S && !(a.causal && key > qi);
-              const float x = ok ? s[n][mt][r] * a.scale : kNegInf;
+              const float x = ok ? s[n][mt][r] : kNegInf;
               s[n][mt][r] = x;
               tmax = fmaxf(tmax, x);
             }
           }
         }
         tmax = max4_groups(tmax);
-        const float m_new = fmaxf(m[n], tmax);
-        // A row with every key so far masked keeps m = -inf (exp(-inf - -inf) would be NaN).
-        const bool none = m_new == kNegInf;
-        const float alpha = none ? 1.0f : exp2_hw((m[n] - m_new) * kLog2e);
+        // The row's reference max m moves only when this tile's max exceeds it by more than
+        // kRescaleLog2 in the exponent (so p <= 2^kRescaleLog2); O and the row sum are rescaled
+        // only when some lane's m moved (wave-uniform). A row with every key so far masked keeps
+        // m = -inf.
+        const bool grow = (m[n] == kNegInf && tmax != kNegInf) || (tmax - m[n]) * c2 > kRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          // (From m = -inf: nothing accumulated yet, alpha 0, also when c2 = 0.)
+          const float alpha = !grow ? 1.0f : m[n] == kNegInf ? 0.0f : exp2_hw((m[n] - tmax) * c2);
+          if (grow) m[n] = tmax;
+          lsum[n] *= alpha;
+#pragma unroll
+          for (int mt = 0; mt < kDT; ++mt) acc[n][mt] *= alpha;
+        }
+        // p = 2^(s c2 - m c2): one fma per score.
+        const float mc = m[n] * c2;
         float psum = 0.0f;
+        if (full) {
 #pragma unroll
-        for (int mt = 0; mt < kFwdSub; ++mt) {
+          for (int mt = 0; mt < kFwdSub; ++mt) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float p = none ? 0.0f : exp2_hw((s[n][mt][r] - m_new) * kLog2e);
-            s[n][mt][r] = p;
-            psum += p;
+            for (int r = 0; r < 4; ++r) {
+              const float p = exp2_hw(fmaf(s[n][mt][r], c2, -mc));
+              s[n][mt][r] = p;
+              psum += p;
+            }
+          }
+        } else {
+          // Masked scores are -inf: select 0 for them (the fma would give NaN for -inf * 0 or
+          // -inf + inf).
+#pragma unroll
+          for (int mt = 0; mt < kFwdSub; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float x = s[n][mt][r];
+              const float p = x == kNegInf ? 0.0f : exp2_hw(fmaf(x, c2, -mc));
+              s[n][mt][r] = p;
+              psum += p;
+            }
           }
         }
-        lsum[n] = lsum[n] * alpha + psum;
-        m[n] = m_new;
-#pragma unroll
-        for (int mt = 0; mt < kDT; ++mt) acc[n][mt] *= alpha;
+        lsum[n] += psum;
       }
 #pragma unroll
       for (int kt = 0; kt < kFwdSub; ++kt) {
@@ -395,7 +426,7 @@ fwd_kernel(FwdArgs a) {
         float* orow = a.o + ((static_cast<int64_t>(b) * S + qi) * a.H + h) * D;
 #pragma unroll
         for (int mt = 0; mt < kDT; ++mt) st4(orow + 16 * mt + 4 * g, acc[n][mt] * inv);
-        if (g == 0) a.lse[static_cast<int64_t>(bh) * S + qi] = m[n] + logf(l);
+        if (g == 0) a.lse[static_cast<int64_t>(bh) * S + qi] = m[n] * ascale + logf(l);
       }
     }
   }

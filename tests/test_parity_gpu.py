@@ -544,3 +544,20 @@ def test_head_dims_kernel_level(orc, cuda, d):
                                scale, 1, st, st, st, gst, stream))
     torch.cuda.synchronize()
     assert torch.equal(o, o_ref) and torch.equal(dqkv, g_ref)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_scale_signs(orc, cuda, causal):
+    """Any finite scale, as the reference takes: negative (the forward's running max is taken on
+    the scaled scores' order), zero (uniform attention) and a large one (peaked softmax)."""
+    rng = np.random.default_rng(11)
+    b, s, h, d = 2, 150, 2, 64
+    x = rng.standard_normal((b, s, 3 * h * d)).astype(np.float32)
+    w = rng.standard_normal((b, s, h * d)).astype(np.float32)
+    qkv, wt = torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda)
+    for scale in (-0.125, 0.0, 0.7):
+        say(f"scale {scale} causal={causal}")
+        ref_out, ref_lse, ref_grad = oracle_qkv(orc, x, w, h, d, causal, np.float64, scale)
+        out, grad = run("fused_qkv", qkv, wt, h, d, causal, scale)
+        floor, _ = composed_floor(orc, x, w, h, d, causal, ref_out, ref_grad, scale)
+        check_errors(orc, out, grad, ref_out, ref_grad, f"scale {scale}", floor)
