@@ -112,7 +112,7 @@ def main() -> int:
                                             sp))
 
     def main_k():
-        _lib.check(L.fattn_bwd_main_f32_d64(qp, kp, vp, P(dout), P(lse), P(dqkv), P(ws),
+        _lib.check(L.fattn_bwd_main_f32_d64(qp, kp, vp, P(out), P(dout), P(lse), P(dqkv), P(ws),
                                             ws_bytes, B, H, S, D, SCALE, ci, qst, qst, qst, gst,
                                             sp))
 
@@ -156,7 +156,8 @@ def main() -> int:
     # Per-kernel durations: K more steps, back to back as above, with the backward launched as
     # its kernel-level steps (the same kernels on the same arguments as fattn_qkv_backward) and a
     # HIP event on the launch stream between every two launches.
-    kernels = [("fwd", fwd), ("bwd_prep", prep_k), ("bwd_main", main_k)]
+    # Step 1 launches nothing with a split workspace at d 64 (step 2 computes D itself).
+    kernels = [("fwd", fwd)] + ([] if split else [("bwd_prep", prep_k)]) + [("bwd_main", main_k)]
     if split:
         kernels.append(("bwd_dq", dq_k))
     marks = []
@@ -172,7 +173,7 @@ def main() -> int:
     kus = {name: statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in marks) * 1e3
            for i, (name, _) in enumerate(kernels)}
     steps_us = statistics.mean(ev[0].elapsed_time(ev[-1]) for ev in marks) * 1e3
-    fwd_us, prep_us, main_us = kus["fwd"], kus["bwd_prep"], kus["bwd_main"]
+    fwd_us, prep_us, main_us = kus["fwd"], kus.get("bwd_prep", 0.0), kus["bwd_main"]
     dq_us = kus.get("bwd_dq", 0.0)
     log(f"bench: kernels fwd {fwd_us:.1f} us, prep {prep_us:.1f} us, bwd main {main_us:.1f} us, "
         f"dq sum {dq_us:.1f} us ({'split' if split else 'turns'}); step {steps_us:.1f} us")

@@ -77,9 +77,9 @@ def _declare(L: ctypes.CDLL) -> None:
                                                       C_INT, A3, A3, A3, P]
         getattr(L, "fattn_bwd_prep_f32" + sfx).argtypes = [P, P, A3, P, SIZE, I64, I64, I64, I64,
                                                            P]
-        getattr(L, "fattn_bwd_main_f32" + sfx).argtypes = [P, P, P, P, P, P, P, SIZE, I64, I64,
-                                                           I64, I64, C_FLOAT, C_INT, A3, A3, A3,
-                                                           A3, P]
+        getattr(L, "fattn_bwd_main_f32" + sfx).argtypes = [P, P, P, P, P, P, P, P, SIZE, I64,
+                                                           I64, I64, I64, C_FLOAT, C_INT, A3, A3,
+                                                           A3, A3, P]
         getattr(L, "fattn_bwd_dq_f32" + sfx).argtypes = [P, P, SIZE, I64, I64, I64, I64, C_FLOAT,
                                                          C_INT, P]
         getattr(L, "fattn_bwd_f32" + sfx).argtypes = [P, P, P, P, P, P, P, P, SIZE, I64, I64, I64,

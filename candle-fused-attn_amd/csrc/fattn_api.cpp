@@ -174,6 +174,8 @@ int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_
   }
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
+  // split (d <= 64): step 2 computes D itself and needs no counters.
+  if (!fattn::bwd_needs_prep(p.part != nullptr, static_cast<int>(d))) return ok();
   const int err = fattn::launch_bwd_prep(o, d_o, p.dsum, p.turn, p.ctrl, static_cast<int>(b),
                                          static_cast<int>(h), static_cast<int>(s),
                                          static_cast<int>(d), stream);
@@ -181,23 +183,23 @@ int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_
   return ok();
 }
 
-int run_bwd_main(const char* who, View q, View k, View v, View d_o, const float* lse,
-                 float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h, int64_t s,
-                 int64_t d, float scale, int causal, void* stream) {
+int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d_o,
+                 const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
+                 int64_t s, int64_t d, float scale, int causal, void* stream) {
   if (int rc = check_range(who, b, h, s, d)) return rc;
   if (!slice_fits(q, s, d) || !slice_fits(d_o, s, d) || s * 3 * h * d > int64_t{UINT32_MAX}) {
     return slice_error(who, s);
   }
-  if (!q.p || !k.p || !v.p || !d_o.p || !lse || !dqkv) {
+  if (!q.p || !k.p || !v.p || !o || !d_o.p || !lse || !dqkv) {
     return fail(FATTN_EINVAL, std::string(who) + ": null operand");
   }
   if (!view_aligned(q) || !view_aligned(k) || !view_aligned(v) || !view_aligned(d_o) ||
-      !aligned16(dqkv)) {
+      !aligned16(o) || !aligned16(dqkv)) {
     return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
   }
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
-  const int err = fattn::launch_bwd_main(q, k, v, d_o, lse, p.dsum, dqkv, p.part, p.turn, p.ctrl,
+  const int err = fattn::launch_bwd_main(q, k, v, d_o, o, lse, p.dsum, dqkv, p.part, p.turn, p.ctrl,
                                          static_cast<int>(b), static_cast<int>(h),
                                          static_cast<int>(s), static_cast<int>(d), scale,
                                          causal ? 1 : 0, stream);
@@ -228,8 +230,8 @@ int run_backward(const char* who, View q, View k, View v, const float* o, View d
                  const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
                  int64_t s, int64_t d, float scale, int causal, void* stream) {
   if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, d, stream)) return rc;
-  if (int rc = run_bwd_main(who, q, k, v, d_o, lse, dqkv, ws, ws_bytes, b, h, s, d, scale, causal,
-                            stream)) {
+  if (int rc = run_bwd_main(who, q, k, v, o, d_o, lse, dqkv, ws, ws_bytes, b, h, s, d, scale,
+                            causal, stream)) {
     return rc;
   }
   return run_bwd_dq(who, dqkv, ws, ws_bytes, b, h, s, d, scale, causal, stream);
@@ -344,11 +346,12 @@ int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_stride
                       workspace_bytes, b, h, s, d, stream);
 }
 
-int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* d_o,
-                       const float* lse, float* dqkv, void* workspace, size_t workspace_bytes,
-                       int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
-                       const int64_t q_strides[3], const int64_t k_strides[3],
-                       const int64_t v_strides[3], const int64_t do_strides[3], void* stream) {
+int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* o,
+                       const float* d_o, const float* lse, float* dqkv, void* workspace,
+                       size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                       float scale, int causal, const int64_t q_strides[3],
+                       const int64_t k_strides[3], const int64_t v_strides[3],
+                       const int64_t do_strides[3], void* stream) {
   if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
   if (int rc = check_head_dim(d)) return rc;
   if (empty3(b, h, s)) return ok();
@@ -356,8 +359,8 @@ int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const flo
     return fail(FATTN_EINVAL, "fused_attention: null strides");
   }
   return run_bwd_main("fused_attention", make_view(q, q_strides), make_view(k, k_strides),
-                      make_view(v, v_strides), make_view(d_o, do_strides), lse, dqkv, workspace,
-                      workspace_bytes, b, h, s, d, scale, causal, stream);
+                      make_view(v, v_strides), o, make_view(d_o, do_strides), lse, dqkv,
+                      workspace, workspace_bytes, b, h, s, d, scale, causal, stream);
 }
 
 int fattn_bwd_dq_f32(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
@@ -403,14 +406,14 @@ int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_st
   return fattn_bwd_prep_f32(o, d_o, do_strides, workspace, workspace_bytes, b, h, s, d, stream);
 }
 
-int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
-                           const float* lse, float* dqkv, void* workspace,
+int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* o,
+                           const float* d_o, const float* lse, float* dqkv, void* workspace,
                            size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
                            float scale, int causal, const int64_t q_strides[3],
                            const int64_t k_strides[3], const int64_t v_strides[3],
                            const int64_t do_strides[3], void* stream) {
   if (int rc = check_head_dim64(d)) return rc;
-  return fattn_bwd_main_f32(q, k, v, d_o, lse, dqkv, workspace, workspace_bytes, b, h, s, d,
+  return fattn_bwd_main_f32(q, k, v, o, d_o, lse, dqkv, workspace, workspace_bytes, b, h, s, d,
                             scale, causal, q_strides, k_strides, v_strides, do_strides, stream);
 }
 

@@ -48,11 +48,11 @@ int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, i
                    float scale, int causal, void* stream);
 int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl, int b, int h,
                     int s, int d, void* stream);
-// part == nullptr: the turn hand-over (dQ final after step 2); else the split partials, which
-// step 3 (launch_bwd_dq) sums into dQ.
-int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
-                    float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s, int d,
-                    float scale, int causal, void* stream);
+// part == nullptr: the turn hand-over (dQ final after step 2; D from step 1); else the split
+// partials, which step 3 (launch_bwd_dq) sums into dQ (D computed from o here, no step 1).
+int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const float* lse,
+                    const float* dsum, float* dqkv, float* part, int* turn, int* ctrl, int b,
+                    int h, int s, int d, float scale, int causal, void* stream);
 int launch_bwd_dq(const float* part, float* dqkv, int b, int h, int s, int d, float scale,
                   int causal, void* stream);
 
@@ -61,6 +61,9 @@ int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal, int d);
 int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s);
 int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d);
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s);
+// Whether step 1 (D, counters) must run: the turn mode, and the split mode at d 128 (its step 2
+// has no LDS room to compute D itself).
+bool bwd_needs_prep(bool split, int d);
 
 }  // namespace fattn
 

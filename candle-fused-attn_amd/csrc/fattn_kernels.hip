@@ -124,8 +124,8 @@ __device__ __forceinline__ int xcd_remap(int id, int total) {
 // empty asm keeps memory accesses from moving across the wait.
 template <int N>
 __device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 16, "vmcnt 0..15");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt 0..63");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   asm volatile("" ::: "memory");
 }
 // Waits until every vector memory operation of this wave has completed (loads returned, stores
@@ -504,8 +504,10 @@ constexpr int kBwdLd = 68;     // dS tile pitch (floats): conflict-free reads an
 
 struct BwdArgs {
   View q, k, v, d_o;
+  const float* o;     // split, D <= 64: the forward's output [b, s, h, D] (D = rowsum(dO o O)
+                      // computed here)
   const float* lse;
-  const float* dsum;
+  const float* dsum;  // otherwise: D from step 1
   float* dqkv;
   float* part;  // split: the dQ partials, [nkb][b h][ntile][kQT * D] in fragment order
   int* turn;
@@ -572,6 +574,10 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   constexpr bool kKtLds = D == 128;
   __shared__ __attribute__((aligned(16))) float sKt[kKtLds ? D * kBwdLd : 4];
   __shared__ __attribute__((aligned(16))) float sQ[2][kQT * D];
+  // split (D <= 64): the O tile, for D = rowsum(dO o O) computed here (step 1 computes it for the
+  // turn mode, and for D 128, whose LDS has no room for O).
+  constexpr bool kFuseD = kSplit && D <= 64;
+  __shared__ __attribute__((aligned(16))) float sO[kFuseD ? 2 : 1][kFuseD ? kQT * D : 4];
   __shared__ __attribute__((aligned(16))) float sdO[2][kQT * D];
   __shared__ __attribute__((aligned(16))) float sdS[kQT * kBwdLd];
   __shared__ __attribute__((aligned(16))) float sL[2][kQT];
@@ -588,6 +594,9 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
     // Causal: round-robin over the XCDs, which spreads the expensive low blocks evenly.
     const int n = static_cast<int>(gridDim.x), id = static_cast<int>(blockIdx.x);
     item = a.causal ? id : xcd_remap(id, n);
+    // No turn waits here: the guard word reads 0 (step 1, which clears it for the turn mode, does
+    // not run for the split mode).
+    if (id == 0 && tid == 0) a.ctrl[kCtrlGuard] = 0;
   } else {
     // Ticket: the key block this workgroup computes, in arrival order. Key block kb of a (b, h)
     // has a later item than kb - 1, so the block it waits on was taken by an earlier, running
@@ -620,6 +629,9 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   const float* kp = a.k.p + b * a.k.sb + h * a.k.sh;
   const float* vp = a.v.p + b * a.v.sb + h * a.v.sh;
   const float* gp = a.d_o.p + b * a.d_o.sb + h * a.d_o.sh;
+  // O [b, s, h, D]: row i of this (b, h) at op + i H D (split only).
+  const float* op = kFuseD ? a.o + (static_cast<int64_t>(b) * S * a.H + h) * D : nullptr;
+  const unsigned o_ss4 = static_cast<unsigned>(a.H) * D * 4u;
   const float* lp = a.lse + static_cast<int64_t>(bh) * S;
   const float* dp = a.dsum + static_cast<int64_t>(bh) * S;
   int* tp = a.turn + static_cast<int64_t>(bh) * a.ntile;
@@ -687,11 +699,35 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
       if (j0 + w < kCopies) {
         copy_part<D>(qp, q_ss4, q0, S - 1, sQ[buf], j0 + w, lane);
         copy_part<D>(gp, g_ss4, q0, S - 1, sdO[buf], j0 + w, lane);
+        if constexpr (kFuseD) copy_part<D>(op, o_ss4, q0, S - 1, sO[buf], j0 + w, lane);
       }
     }
-    if (w < 2 && lane < kQT) {
-      const unsigned off = 4u * static_cast<unsigned>(min(q0 + lane, S - 1));
-      load_lds4(w == 0 ? lp : dp, off, w == 0 ? sL[buf] : sD[buf]);
+    if (kFuseD ? w == 0 : w < 2) {
+      if (lane < kQT) {
+        const unsigned off = 4u * static_cast<unsigned>(min(q0 + lane, S - 1));
+        load_lds4(w == 0 ? lp : dp, off, w == 0 ? sL[buf] : sD[buf]);
+      }
+    }
+  };
+  // kFuseD: D of the tile in buffer `buf` from its staged O and dO rows, into sD[buf]. D / 4 lanes
+  // per row, the same operations in the same order as step 1 (prep_kernel), so D is the same.
+  auto rowsum_do_o = [&](int buf) {
+    constexpr int kLanes = D / 4;
+#pragma unroll
+    for (int i0 = 0; i0 < kQT * kLanes; i0 += kThreads) {
+      const int i = i0 + tid, row = i / kLanes, c4 = i % kLanes;
+      float x = 0.0f;
+      if (i < kQT * kLanes) {
+        const f4 ov = ld4(&sO[kFuseD ? buf : 0][swz<D>(row, 4 * c4)]);
+        const f4 gv = ld4(&sdO[buf][swz<D>(row, 4 * c4)]);
+        x = ov.x * gv.x;
+        x = fmaf(ov.y, gv.y, x);
+        x = fmaf(ov.z, gv.z, x);
+        x = fmaf(ov.w, gv.w, x);
+      }
+#pragma unroll
+      for (int k = kLanes / 2; k >= 1; k /= 2) x += __shfl_xor(x, k);
+      if (i < kQT * kLanes && c4 == 0) sD[buf][row] = x;
     }
   };
   // The order in which key blocks add into a tile's dQ (fixed by the shape alone, so every run
@@ -815,6 +851,10 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   gload(tile_at(0) * kQT, 0);
   wait_stores();  // the direct copies have landed
   __syncthreads();
+  if constexpr (kFuseD) {
+    rowsum_do_o(0);
+    __syncthreads();
+  }
   // One tile; `bufc()` is the LDS buffer, t % 2. The split kernel unrolls the walk by two so that
   // it is a compile-time constant there and LDS addresses fold the buffer offset into the
   // instruction (the turn kernel has no registers to spare for that).
@@ -975,7 +1015,10 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
     p1_q0 = q0;
     p1_pos = pos_of(q0 / kQT);
     p1_cnt = count_of(q0 / kQT);
-    __syncthreads();  // dS read by every wave
+    if constexpr (kFuseD) {
+      if (has_next) rowsum_do_o(buf ^ 1);  // the next tile's D (its rows landed before the barrier)
+    }
+    __syncthreads();  // dS read by every wave; the next tile's D written
   };
   if constexpr (kSplit) {
     for (int t = 0; t < nsteps; t += 2) {
@@ -1130,6 +1173,7 @@ int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d) {
   return (b * h * s + rows_per_block - 1) / rows_per_block;
 }
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQT - 1) / kQT); }
+bool bwd_needs_prep(bool split, int d) { return !split || d > 64; }
 
 int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s, int d,
                    float scale, int causal, void* stream) {
@@ -1153,13 +1197,13 @@ int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl,
   return static_cast<int>(launch(fn, bwd_prep_blocks(b, h, s, d), args, stream));
 }
 
-int launch_bwd_main(View q, View k, View v, View d_o, const float* lse, const float* dsum,
-                    float* dqkv, float* part, int* turn, int* ctrl, int b, int h, int s, int d,
-                    float scale, int causal, void* stream) {
+int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const float* lse,
+                    const float* dsum, float* dqkv, float* part, int* turn, int* ctrl, int b,
+                    int h, int s, int d, float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
   const bool split = part != nullptr;
   const int stagger = !split && !causal && nkb <= kStaggerMaxBlocks ? 1 : 0;
-  BwdArgs a{q, k, v, d_o, lse, dsum, dqkv, part, turn, ctrl, b, h, s,
+  BwdArgs a{q, k, v, d_o, o, lse, dsum, dqkv, part, turn, ctrl, b, h, s,
             nkb, ntile, scale, causal, stagger};
   void* args[] = {&a};
   const void* fn;

@@ -82,22 +82,27 @@ size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s, int64_t d)
 size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s, int64_t d);
 
 /* Backward step 1: D[b, h, i] = sum_c dO[b, i, h, c] * O[b, i, h, c] (fixed order) and the
- * counters of step 2 cleared. O is [b, s, h, d] contiguous; dO is read through do_strides.
- * Replaces the fattn_bwd_dot_f32_d64 launch (src/cuda.rs:215-231). */
+ * counters of step 2 cleared. O is [b, s, h, d] contiguous; dO is read through do_strides. With
+ * a split-size workspace there is nothing to do (step 2 computes D itself; returns 0 after the
+ * checks; d 128 still needs this step). Replaces the fattn_bwd_dot_f32_d64 launch
+ * (src/cuda.rs:215-231). */
 int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_strides[3],
                        void* workspace, size_t workspace_bytes, int64_t b, int64_t h, int64_t s,
                        int64_t d, void* stream);
 
 /* Backward step 2: dK and dV into ONE [b, s, 3, h, d] buffer (the fused qkv projection's
  * gradient layout); dQ summed over key blocks in a fixed order, so every rerun is bit-identical:
- * with a split-size workspace its partials go to the workspace (step 3 finishes dQ), else dQ is
- * complete after this step. Needs step 1 on the same workspace first. Replaces the
- * fattn_bwd_f32_d64 launch (src/cuda.rs:233-258). */
-int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* d_o,
-                       const float* lse, float* dqkv, void* workspace, size_t workspace_bytes,
-                       int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,
-                       const int64_t q_strides[3], const int64_t k_strides[3],
-                       const int64_t v_strides[3], const int64_t do_strides[3], void* stream);
+ * with a split-size workspace its partials go to the workspace (step 3 finishes dQ) and, for
+ * d <= 64, D is computed here from O (the forward's [b, s, h, d] output); else dQ is complete
+ * after this step. Where D is not computed here it comes from step 1, which must run first on
+ * the same workspace (running step 1 first is always correct). Replaces the
+ * fattn_bwd_f32_d64 launch (src/cuda.rs:233-258), which takes no O. */
+int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* o,
+                       const float* d_o, const float* lse, float* dqkv, void* workspace,
+                       size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
+                       float scale, int causal, const int64_t q_strides[3],
+                       const int64_t k_strides[3], const int64_t v_strides[3],
+                       const int64_t do_strides[3], void* stream);
 
 /* Backward step 3: with a split-size workspace, dQ = scale * (sum of step 2's partials in
  * key-block order) into part 0 of dqkv; with a smaller one nothing to do (returns 0). Has no
@@ -122,8 +127,8 @@ int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, 
 int fattn_bwd_prep_f32_d64(const float* o, const float* d_o, const int64_t do_strides[3],
                            void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                            int64_t s, int64_t d, void* stream);
-int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* d_o,
-                           const float* lse, float* dqkv, void* workspace,
+int fattn_bwd_main_f32_d64(const float* q, const float* k, const float* v, const float* o,
+                           const float* d_o, const float* lse, float* dqkv, void* workspace,
                            size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
                            float scale, int causal, const int64_t q_strides[3],
                            const int64_t k_strides[3], const int64_t v_strides[3],

@@ -314,7 +314,7 @@ def test_kernel_level_entry_points(orc, cuda):
         ws = torch.empty(n, dtype=torch.uint8, device=cuda)
         dqkv = torch.empty_like(qkv)
         _lib.check(L.fattn_bwd_prep_f32_d64(P(o), P(wt), gst, P(ws), n, b, h, s, d, stream))
-        _lib.check(L.fattn_bwd_main_f32_d64(qp, kp, vp, P(wt), P(lse), P(dqkv), P(ws), n, b, h,
+        _lib.check(L.fattn_bwd_main_f32_d64(qp, kp, vp, P(o), P(wt), P(lse), P(dqkv), P(ws), n, b, h,
                                             s, d, scale, 1, st, st, st, gst, stream))
         _lib.check(L.fattn_bwd_dq_f32_d64(P(dqkv), P(ws), n, b, h, s, d, scale, 1, stream))
         torch.cuda.synchronize()
