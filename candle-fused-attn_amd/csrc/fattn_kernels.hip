@@ -1084,8 +1084,18 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
   const float* src = part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D);
 #pragma unroll
   for (int i = tid; i < kF4; i += kThreads) {
+    // Loads four slots at a time (independent), adds them in key-block order.
     f4 acc = ld4(src + 4 * i);
-    for (int kb = 1; kb < cnt; ++kb) acc += ld4(src + kb * slot + 4 * i);
+    int kb = 1;
+    for (; kb + 3 < cnt; kb += 4) {
+      const f4 x0 = ld4(src + kb * slot + 4 * i), x1 = ld4(src + (kb + 1) * slot + 4 * i);
+      const f4 x2 = ld4(src + (kb + 2) * slot + 4 * i), x3 = ld4(src + (kb + 3) * slot + 4 * i);
+      acc += x0;
+      acc += x1;
+      acc += x2;
+      acc += x3;
+    }
+    for (; kb < cnt; ++kb) acc += ld4(src + kb * slot + 4 * i);
     acc *= scale;
     const int lane = i & 63, md = i >> 6, dt = md % kDT, m = md / kDT;
     const int lo = lane & 15, g = lane >> 4;
