@@ -69,6 +69,30 @@ __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<con
 __device__ __forceinline__ void st4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
 __device__ __forceinline__ f4 zero4() { return f4{0.0f, 0.0f, 0.0f, 0.0f}; }
 
+// A lane of x through a DPP lane permutation (VALU, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Sum over each aligned group of N = 8, 16 or 32 lanes, every lane of the group getting the same
+// bits (each step adds a lane and its partner, and x + y == y + x): partner = lane ^ 1
+// (quad_perm 1,0,3,2), lane ^ 2 (quad_perm 2,3,0,1), the other quad of the 8 (row_half_mirror),
+// the other 8 of the 16 (row_mirror), the other 16 of the 32 (row swap).
+template <int N>
+__device__ __forceinline__ float lane_sum(float x) {
+  static_assert(N == 8 || N == 16 || N == 32, "groups of 8, 16 or 32 lanes");
+  x += dpp<0xB1>(x);
+  x += dpp<0x4E>(x);
+  x += dpp<0x141>(x);
+  if constexpr (N >= 16) x += dpp<0x140>(x);
+  if constexpr (N == 32) {
+    const unsigned u = __float_as_uint(x);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  }
+  return x;
+}
+
 // max over lanes lo, lo + 16, lo + 32, lo + 48 (every lane gets it), on the VALU: the gfx950 row
 // swaps pair row r of one operand with row r ^ 1 (16-lane rows), then half h with h ^ 1
 // (32-lane halves); with both operands x, the max of the two results is the max of each pair.
@@ -434,8 +458,8 @@ fwd_kernel(FwdArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // Backward, step 1: D[b, h, i] = sum_c dO[b, i, h, c] O[b, i, h, c]. D / 4 lanes per row (one
-// float4 each, then the xor butterfly D / 8, ..., 2, 1: one fixed order). It also clears the turn
-// counters, the ticket and the guard word of step 2 (stream order puts it first).
+// float4 each, then lane_sum: one fixed order). It also clears the turn counters, the ticket and
+// the guard word of step 2 (stream order puts it first).
 // ---------------------------------------------------------------------------------------------
 template <int D>
 __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict__ o, View d_o,
@@ -462,8 +486,7 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
     x = fmaf(ov.z, gv.z, x);
     x = fmaf(ov.w, gv.w, x);
   }
-#pragma unroll
-  for (int k = kLanes / 2; k >= 1; k /= 2) x += __shfl_xor(x, k);
+  x = lane_sum<kLanes>(x);
   if (row < rows && c4 == 0) dsum[row] = x;
 }
 
@@ -725,8 +748,7 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
         x = fmaf(ov.z, gv.z, x);
         x = fmaf(ov.w, gv.w, x);
       }
-#pragma unroll
-      for (int k = kLanes / 2; k >= 1; k /= 2) x += __shfl_xor(x, k);
+      x = lane_sum<kLanes>(x);
       if (i < kQT * kLanes && c4 == 0) sD[buf][row] = x;
     }
   };
