@@ -157,15 +157,22 @@ __device__ __forceinline__ void wait_vm() {
 __device__ __forceinline__ void wait_mem() { wait_vm<0>(); }
 
 // Tiles staged by direct copies are [rows][D floats], unpadded, in 16-byte chunks; chunk c of row
-// r sits at position c ^ f(r), which keeps both read patterns used on them free of bank
-// conflicts: row-wise float4 reads (16 lanes on 16 rows, the same chunk each: the 16 positions
-// must fall in distinct 16-byte bank groups of 256 bytes) and column reads (lanes across 4 rows x
-// 16 consecutive floats). f(r) = r % 16 for D 64 and 128 (rows are multiples of 256 bytes);
-// D 32 (128-byte rows: two rows per 256 bytes) uses f(r) = (r / 2) % 8, conflict-free for the row
-// reads, 2-way for the column reads (64 lanes over 4 rows of 128 bytes cannot do better).
+// r sits at position c ^ f(r). Three read patterns hit these tiles: row-wise float4 reads (lane
+// (lo, g) reads row lo, chunk 4 g + u), float reads down columns (lane (lo, g): row 4 g + r,
+// column 16 t + lo) and the row sums' float4 reads (16 lanes on one row, 4 rows per wave).
+// On MI355X (measured with the SQ_LDS_BANK_CONFLICT counter on probe kernels): float reads are
+// conflict-free when the 32 lanes of each half-wave hit 32 distinct dword banks (address mod
+// 128 bytes); float4 reads follow no simple bank model, so f was chosen by measurement. For
+// 256-byte rows (D 64) f is XOR-linear in the bits of r % 16 with f(1) = 3, f(2) = 9, f(4) = 12,
+// f(8) = 2 (the 16 values packed in kSwz64): all three patterns conflict-free, where
+// f(r) = r % 16 left the row-wise float4 reads 2-way. D 128 keeps f(r) = r % 16; D 32 (128-byte
+// rows) uses f(r) = (r / 2) % 8.
+constexpr unsigned long long kSwz64 = 0x47de8b1265fca930ull;
 template <int D>
 __device__ __forceinline__ int swz_f(int row) {
-  return D == 32 ? ((row >> 1) & 7) : (row & 15);
+  if constexpr (D == 32) return (row >> 1) & 7;
+  if constexpr (D == 64) return static_cast<int>((kSwz64 >> (4 * (row & 15))) & 15);
+  return row & 15;
 }
 template <int D>
 __device__ __forceinline__ int swz(int row, int col) {
@@ -522,7 +529,7 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
 #endif
 constexpr int kQT = kBwdQueryTile;
 constexpr int kNS = kQT / 16;  // 16-query subtiles per tile
-constexpr int kBwdLd = 68;     // dS tile pitch (floats): conflict-free reads and writes
+constexpr int kBwdLd = 68;     // pitch (floats) of the transposed K tile at D 128
 // Q and dO tiles are [kQT rows][D floats] in the swizzled layout of swz(), filled by direct copies.
 
 struct BwdArgs {
@@ -602,7 +609,9 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   constexpr bool kFuseD = kSplit && D <= 64;
   __shared__ __attribute__((aligned(16))) float sO[kFuseD ? 2 : 1][kFuseD ? kQT * D : 4];
   __shared__ __attribute__((aligned(16))) float sdO[2][kQT * D];
-  __shared__ __attribute__((aligned(16))) float sdS[kQT * kBwdLd];
+  // dS [kQT][64 keys], swizzled like a D 64 tile (its writes are column reads' pattern, its
+  // reads row-wise float4 reads).
+  __shared__ __attribute__((aligned(16))) float sdS[kQT * kBwdKeys];
   __shared__ __attribute__((aligned(16))) float sL[2][kQT];
   __shared__ __attribute__((aligned(16))) float sD[2][kQT];
   __shared__ int s_item;
@@ -975,7 +984,7 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 #pragma unroll
     for (int m = 0; m < kNS; ++m) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sdS[(16 * m + 4 * g + r) * kBwdLd + 16 * w + lo] = sP[m][r];
+      for (int r = 0; r < 4; ++r) sdS[swz<kBwdKeys>(16 * m + 4 * g + r, 16 * w + lo)] = sP[m][r];
     }
     if (kSplit) {
       // The next tile's copies complete (the partial's stores, issued after them, need not).
@@ -1015,10 +1024,9 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 #pragma unroll
       for (int j = 0; j < kDQ; ++j) p1[j][m] = zero4();
       if (q0 + 16 * m >= S || !wave_dq) continue;
-      const float* sr = sdS + (16 * m + lo) * kBwdLd + 16 * g;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const f4 x = ld4(sr + 4 * u);
+        const f4 x = ld4(&sdS[swz<kBwdKeys>(16 * m + lo, 16 * g + 4 * u)]);
 #pragma unroll
         for (int j = 0; j < kDQ; ++j) {
           f4 y;
