@@ -32,6 +32,7 @@
 //     dispatch order). Needs no workspace beyond D and the counters.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include "fattn_internal.h"
@@ -43,6 +44,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // An int known at compile time, or not, behind the same call syntax.
 template <int V>
 struct Const {
+  static constexpr int value = V;
   __device__ constexpr int operator()() const { return V; }
 };
 struct Var {
@@ -105,6 +107,72 @@ __device__ __forceinline__ float max4_groups(float x) {
   return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 
+// v_permlane16_swap / v_permlane32_swap on a pair of floats (16-lane rows: the first swaps odd
+// rows of a with even rows of b, the second the upper 32 lanes of a with the lower 32 of b).
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                  false);
+  a = __uint_as_float(p[0]);
+  b = __uint_as_float(p[1]);
+}
+__device__ __forceinline__ void swap_rows32(float& a, float& b) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                  false);
+  a = __uint_as_float(p[0]);
+  b = __uint_as_float(p[1]);
+}
+// 4 x 4 transpose of float4 blocks across the lane groups g: afterwards x[j] of lane (lo, g) is
+// what x[g] of lane (lo, j) was.
+__device__ __forceinline__ void transpose_groups(f4& x0, f4& x1, f4& x2, f4& x3) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float a = x0[e], b = x1[e], c = x2[e], d = x3[e];
+    swap_rows16(a, b);
+    swap_rows16(c, d);
+    swap_rows32(a, c);
+    swap_rows32(b, d);
+    x0[e] = a;
+    x1[e] = b;
+    x2[e] = c;
+    x3[e] = d;
+  }
+}
+// The register operand of the products over head_dim: dst[t] = row[D / 4 g + t] (lane (lo, g)
+// holds quarter g of its row). At D 64 and 128 the row is read in whole 64-byte sectors -- load u
+// of lane group g reads dims 16 u + 4 g .. + 3, so the four groups' loads of one row are 64
+// contiguous bytes -- and 4 x 4 transposes across the lane groups move every float4 to its
+// quarter's group (D 64: one transpose; D 128: one over the even loads, one over the odd). At D 32
+// each lane reads its quarter directly (two float4s). Every lane of the wave must execute it.
+template <int D>
+__device__ __forceinline__ void load_quarter(const float* row, int g, float (&dst)[D / 4]) {
+  if constexpr (D == 32) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const f4 x = ld4(row + 8 * g + 4 * u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[4 * u + e] = x[e];
+    }
+  } else {
+    constexpr int kU = D / 16;
+    f4 x[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) x[u] = ld4(row + 16 * u + 4 * g);
+    if constexpr (D == 64) {
+      transpose_groups(x[0], x[1], x[2], x[3]);
+    } else {
+      transpose_groups(x[0], x[2], x[4], x[6]);
+      transpose_groups(x[1], x[3], x[5], x[7]);
+    }
+#pragma unroll
+    for (int j = 0; j < kU; ++j) {
+      // D 64: x[j] holds dims 16 g + 4 j; D 128: x[2 i] dims 32 g + 4 i, x[2 i + 1] 32 g + 16 + 4 i.
+      const int at = D == 64 ? 4 * j : (j % 2 == 0 ? 2 * j : 16 + 2 * (j - 1));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[at + e] = x[j][e];
+    }
+  }
+}
+
 typedef __attribute__((address_space(3))) float lds_float;
 // Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane i's 16 bytes land
 // at `lds_base` + 16 i (M0 holds the wave-uniform LDS address). Completion is counted by vmcnt,
@@ -120,6 +188,26 @@ __device__ __forceinline__ void load_lds16(const float* base, unsigned byte_off,
                :
                : "v"(byte_off), "s"(base), "s"(lds)
                : "memory");
+}
+
+// The same with the destination as an LDS byte address (wave-uniform).
+__device__ __forceinline__ void load_lds16_at(const float* base, unsigned byte_off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(byte_off), "s"(base), "s"(lds)
+               : "memory");
+}
+__device__ __forceinline__ void load_lds4_at(const float* base, unsigned byte_off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(byte_off), "s"(base), "s"(lds)
+               : "memory");
+}
+// The LDS byte address of an LDS object (wave-uniform).
+template <typename T>
+__device__ __forceinline__ unsigned lds_addr(T* p) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) T*)p)));
 }
 
 // The same for 4 bytes per lane (global_load_lds_dword): lane i's 4 bytes land at `lds_base` + 4 i;
@@ -193,6 +281,16 @@ __device__ __forceinline__ void copy_part(const float* base, unsigned row_bytes,
   const unsigned src_row = static_cast<unsigned>(min(first_row + row, last_row));
   const unsigned c16 = 16u * static_cast<unsigned>(((lane % kC) ^ swz_f<D>(row)) & (kC - 1));
   load_lds16(base, src_row * row_bytes + c16, dst + kCopyRows<D> * j * D);
+}
+// The same with the tile's LDS byte address.
+template <int D>
+__device__ __forceinline__ void copy_part_at(const float* base, unsigned row_bytes, int first_row,
+                                             int last_row, unsigned dst, int j, int lane) {
+  constexpr int kC = D / 4;
+  const int row = kCopyRows<D> * j + lane / kC;
+  const unsigned src_row = static_cast<unsigned>(min(first_row + row, last_row));
+  const unsigned c16 = 16u * static_cast<unsigned>(((lane % kC) ^ swz_f<D>(row)) & (kC - 1));
+  load_lds16_at(base, src_row * row_bytes + c16, dst + 4u * kCopyRows<D> * j * D);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -271,20 +369,9 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int n = 0; n < kFwdNT; ++n) {
     const int qi = qw0 + 16 * n + lo;
-    if (qi < S) {
-      const float* r = qp + qi * a.q.ss + kQR * g;
+    load_quarter<D>(qp + min(qi, S - 1) * a.q.ss, g, qr[n]);
 #pragma unroll
-      for (int u = 0; u < kQR / 4; ++u) {
-        const f4 x = ld4(r + 4 * u) * qsign;
-        qr[n][4 * u] = x.x;
-        qr[n][4 * u + 1] = x.y;
-        qr[n][4 * u + 2] = x.z;
-        qr[n][4 * u + 3] = x.w;
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < kQR; ++t) qr[n][t] = 0.0f;
-    }
+    for (int t = 0; t < kQR; ++t) qr[n][t] = qi < S ? qr[n][t] * qsign : 0.0f;
   }
 
   // Scores enter the exponent as s * c2 (c2 = |scale| log2 e); m holds raw-score maxima.
@@ -679,26 +766,14 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   // B operands of S and dP: K[key][D/4 g .. D/4 g + D/4 - 1], V likewise; of the dQ product:
   // kQ[j][t] = K[k0 + 16 g + t][16 (w + 4 j) + lo]. Zero past S.
   float kB[kKR], vB[kKR], kQ[kKtLds ? 1 : kDQ][16];
-  if (key < S) {
-    const float* kr = kp + key * a.k.ss + kKR * g;
-    const float* vr = vp + key * a.v.ss + kKR * g;
-#pragma unroll
-    for (int u = 0; u < kKR / 4; ++u) {
-      const f4 x = ld4(kr + 4 * u), y = ld4(vr + 4 * u);
-      kB[4 * u] = x.x;
-      kB[4 * u + 1] = x.y;
-      kB[4 * u + 2] = x.z;
-      kB[4 * u + 3] = x.w;
-      vB[4 * u] = y.x;
-      vB[4 * u + 1] = y.y;
-      vB[4 * u + 2] = y.z;
-      vB[4 * u + 3] = y.w;
-    }
-  } else {
+  {
+    const int kr = min(key, S - 1);
+    load_quarter<D>(kp + kr * a.k.ss, g, kB);
+    load_quarter<D>(vp + kr * a.v.ss, g, vB);
 #pragma unroll
     for (int t = 0; t < kKR; ++t) {
-      kB[t] = 0.0f;
-      vB[t] = 0.0f;
+      kB[t] = key < S ? kB[t] : 0.0f;
+      vB[t] = key < S ? vB[t] : 0.0f;
     }
   }
   if constexpr (kKtLds) {
@@ -1090,6 +1165,268 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 }
 
 // ---------------------------------------------------------------------------------------------
+// Backward, step 2 with the split dQ sum at D <= 64. The products, tile shapes, operand layouts and
+// results are those of bwd_kernel<true, D> (the same operations in the same order, so the outputs
+// are bit-identical); what changes is the schedule, which the split mode leaves free because no
+// workgroup waits on another: one barrier per query tile instead of two. The staged tiles (Q, dO,
+// O, L), D and dS have three LDS buffers (tile t in buffer t % 3). The copies of tile t + 2 are
+// issued at the start of tile t and complete before tile t's barrier; after it, D of tile t + 2 is
+// formed from its staged O and dO rows. So D of a tile is written two barriers before it is read,
+// a tile's buffers are refilled only after the barrier that follows their last read, and a dS
+// buffer is rewritten three tiles after it was written (its readers passed two barriers since).
+// All LDS tiles sit in one array, so that each is a constant offset from one base: the compiler
+// folds such offsets into the LDS instructions, where across separate arrays it keeps an address
+// register per array (at D 64 that saves 24 registers).
+// ---------------------------------------------------------------------------------------------
+template <int D>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BWD_WAVES)))
+bwd_split_kernel(BwdArgs a) {
+  static_assert(D <= 64, "D 128 has no LDS room for three buffers: bwd_kernel<true, 128>");
+  static_assert(kNS == 1, "one 16-query subtile per tile");
+  constexpr int kKR = D / 4;                  // K (or V) values per lane: B operands of S, dP
+  constexpr int kDT = D / 16;                 // 16-dim tiles (dK, dV accumulators; dQ tiles)
+  constexpr int kCopies = kQT / kCopyRows<D>;  // direct copies per Q (or dO, O) tile
+  constexpr int kNB = 3;                      // LDS buffers of the staged tiles, D and dS
+  typedef float Tile[kQT * D];
+  struct Smem {
+    Tile q[kNB], g[kNB], o[kNB];
+    float ds[kNB][kQT * kBwdKeys];
+    float l[kNB][kQT], d[kNB][kQT];
+  };
+  __shared__ __attribute__((aligned(16))) Smem sm;
+  auto& sQ = sm.q;
+  auto& sdO = sm.g;
+  auto& sO = sm.o;
+  auto& sdS = sm.ds;
+  auto& sL = sm.l;
+  auto& sD = sm.d;
+  const unsigned lds0 = lds_addr(&sm);  // LDS byte address of the tiles
+
+  const int tid = threadIdx.x, lane = tid & 63, lo = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
+  const int BH = a.B * a.H, S = a.S;
+  const int id = static_cast<int>(blockIdx.x);
+  const bool wave_dq = w < kDT;  // the wave computes dQ tiles (all waves but 2, 3 at D 32)
+  // No turn waits here: the guard word reads 0.
+  if (id == 0 && tid == 0) a.ctrl[kCtrlGuard] = 0;
+
+  // The key block: non-causal, (b, h)-major with the key blocks of one (b, h) on one XCD (they
+  // read the same Q and dO tiles at about the same time); causal, key-block-major round-robin over
+  // the XCDs (the expensive low blocks start first, spread evenly). Its walk: non-causal every
+  // query tile, causal from the tile of the block's first key on.
+  const int item = a.causal ? id : xcd_remap(id, static_cast<int>(gridDim.x));
+  const int bh = a.causal ? item % BH : item / a.nkb;
+  const int kb = a.causal ? item / BH : item % a.nkb;
+  const int b = bh / a.H, h = bh % a.H;
+  const int k0 = kb * kBwdKeys;
+  const int kw0 = k0 + 16 * w;  // the wave's first key
+  const int key = kw0 + lo;     // this lane's key
+  const int t0 = a.causal ? k0 / kQT : 0;
+  const int nsteps = a.ntile - t0;
+
+  const float* qp = a.q.p + b * a.q.sb + h * a.q.sh;
+  const float* kp = a.k.p + b * a.k.sb + h * a.k.sh;
+  const float* vp = a.v.p + b * a.v.sb + h * a.v.sh;
+  const float* gp = a.d_o.p + b * a.d_o.sb + h * a.d_o.sh;
+  const float* op = a.o + (static_cast<int64_t>(b) * S * a.H + h) * D;
+  const float* lp = a.lse + static_cast<int64_t>(bh) * S;
+  const unsigned q_ss4 = static_cast<unsigned>(a.q.ss) * 4u;
+  const unsigned g_ss4 = static_cast<unsigned>(a.d_o.ss) * 4u;
+  const unsigned o_ss4 = static_cast<unsigned>(a.H) * D * 4u;
+
+  // K, V of this lane's key (B operands of S and dP) and kQ[t] = K[k0 + 16 g + t][16 w + lo]
+  // (B operand of the dQ product), zero past S.
+  float kB[kKR], vB[kKR], kQ[16];
+  {
+    const int kr = min(key, S - 1);
+    load_quarter<D>(kp + kr * a.k.ss, g, kB);
+    load_quarter<D>(vp + kr * a.v.ss, g, vB);
+#pragma unroll
+    for (int t = 0; t < kKR; ++t) {
+      kB[t] = key < S ? kB[t] : 0.0f;
+      vB[t] = key < S ? vB[t] : 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int kk = k0 + 16 * g + t;
+      kQ[t] = kk < S && wave_dq ? kp[min(kk, S - 1) * a.k.ss + 16 * w + lo] : 0.0f;
+    }
+  }
+
+  // Staging of the query tile of walk step t into buffer `buf` (direct copies only; wave 0 copies
+  // L): wave w issues copies w, w + 4, ... of the Q, dO and O tiles; rows past S repeat row S - 1.
+  auto gload = [&](int t, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    const int q0 = (t0 + t) * kQT;
+#pragma unroll
+    for (int j0 = 0; j0 < kCopies; j0 += 4) {
+      if (j0 + w < kCopies) {
+        copy_part_at<D>(qp, q_ss4, q0, S - 1, lds0 + offsetof(Smem, q[buf]), j0 + w, lane);
+        copy_part_at<D>(gp, g_ss4, q0, S - 1, lds0 + offsetof(Smem, g[buf]), j0 + w, lane);
+        copy_part_at<D>(op, o_ss4, q0, S - 1, lds0 + offsetof(Smem, o[buf]), j0 + w, lane);
+      }
+    }
+    if (w == 0 && lane < kQT) {
+      load_lds4_at(lp, 4u * static_cast<unsigned>(min(q0 + lane, S - 1)),
+                   lds0 + offsetof(Smem, l[buf]));
+    }
+  };
+  // D of the tile in buffer `buf` from its staged O and dO rows (as step 1: D / 4 lanes per row,
+  // the same operations in the same order).
+  auto rowsum_do_o = [&](auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    constexpr int kLanes = D / 4;
+#pragma unroll
+    for (int i0 = 0; i0 < kQT * kLanes; i0 += kThreads) {
+      const int i = i0 + tid, row = i / kLanes, c4 = i % kLanes;
+      float x = 0.0f;
+      if (i < kQT * kLanes) {
+        const f4 ov = ld4(&sO[buf][swz<D>(row, 4 * c4)]);
+        const f4 gv = ld4(&sdO[buf][swz<D>(row, 4 * c4)]);
+        x = ov.x * gv.x;
+        x = fmaf(ov.y, gv.y, x);
+        x = fmaf(ov.z, gv.z, x);
+        x = fmaf(ov.w, gv.w, x);
+      }
+      x = lane_sum<kLanes>(x);
+      if (i < kQT * kLanes && c4 == 0) sD[buf][row] = x;
+    }
+  };
+
+  // The dQ partial of query tile j: the wave's 16 x 16 fragment (dim tile w) in the key block's
+  // slot, fragment order (register r of lane (lo, g) at 4 lane + r: query 16 j + 4 g + r, dim
+  // 16 w + lo); step 3 (dq_kernel) sums the slots.
+  float* const slot = a.part + (static_cast<int64_t>(kb) * BH + bh) * a.ntile * (kQT * D) +
+                      256 * w + 4 * lane;
+
+  f4 dva[kDT], dka[kDT];
+#pragma unroll
+  for (int mt = 0; mt < kDT; ++mt) {
+    dva[mt] = zero4();
+    dka[mt] = zero4();
+  }
+  f4 p1 = zero4();  // the dQ fragment of the last tile (stored at the start of the next)
+  auto store_frag = [&](int j) { st4(slot + j * (kQT * D), p1); };
+
+  gload(0, Const<0>{});
+  if (nsteps > 1) gload(1, Const<1>{});
+  wait_mem();  // the direct copies have landed
+  __syncthreads();
+  rowsum_do_o(Const<0>{});
+  if (nsteps > 1) rowsum_do_o(Const<1>{});
+  __syncthreads();
+
+  auto tile_step = [&](auto bufc, int t) {
+    constexpr int buf = decltype(bufc)::value;
+    const int jt = t0 + t;  // query tile
+    const int q0 = jt * kQT;
+    // Tile t + 2 into the buffer of tile t - 1, whose last readers passed the last barrier.
+    if (t + 2 < nsteps) gload(t + 2, Const<(buf + 2) % kNB>{});
+    const bool frag_pending = t > 0 && wave_dq;  // the last tile's fragment is unstored
+    if (frag_pending) store_frag(jt - 1);
+    compiler_fence();
+    const float* Qt = sQ[buf];
+    const float* Gt = sdO[buf];
+
+    // Wave-uniform liveness of this wave's 16 keys for the tile's 16 queries.
+    const bool live = q0 < S && kw0 < S && !(a.causal && kw0 > q0 + 15);
+
+    // S and dP.
+    f4 sS = zero4(), sP = zero4();
+    if (live) {
+#pragma unroll
+      for (int u = 0; u < kKR / 4; ++u) {
+        const int at = swz<D>(lo, kKR * g + 4 * u);
+        const f4 x = ld4(Qt + at), y = ld4(Gt + at);
+        sS = mma(x.x, kB[4 * u], sS);
+        sS = mma(x.y, kB[4 * u + 1], sS);
+        sS = mma(x.z, kB[4 * u + 2], sS);
+        sS = mma(x.w, kB[4 * u + 3], sS);
+        sP = mma(y.x, vB[4 * u], sP);
+        sP = mma(y.y, vB[4 * u + 1], sP);
+        sP = mma(y.z, vB[4 * u + 2], sP);
+        sP = mma(y.w, vB[4 * u + 3], sP);
+      }
+
+      // P = exp(S scale - L), dS = P o (dP - D); lane (lo, g), register r: query q0 + 4 g + r,
+      // key `key`. Then dV^T and dK^T.
+      const f4 Lv = ld4(&sL[buf][4 * g]), Dv = ld4(&sD[buf][4 * g]);
+      const int qi0 = q0 + 4 * g;
+      if (!a.causal && q0 + 16 <= S && kw0 + 16 <= S) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = exp2_hw(fmaf(sS[r], a.scale, -Lv[r]) * kLog2e);
+          sP[r] = p * (sP[r] - Dv[r]);  // dS
+          sS[r] = p;                     // P
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = qi0 + r < S && key < S && !(a.causal && key > qi0 + r);
+          const float e = exp2_hw(fmaf(sS[r], a.scale, -Lv[r]) * kLog2e);
+          const float p = ok ? e : 0.0f;
+          sP[r] = p * (sP[r] - Dv[r]);  // dS
+          sS[r] = p;                     // P
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int mt = 0; mt < kDT; ++mt) {
+          const int at = swz<D>(4 * g + r, 16 * mt + lo);
+          dva[mt] = mma(Gt[at], sS[r], dva[mt]);
+          dka[mt] = mma(Qt[at], sP[r], dka[mt]);
+        }
+      }
+    }
+
+    // This tile's dS into LDS (zero where the wave's keys are all masked).
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sdS[buf][swz<kBwdKeys>(4 * g + r, 16 * w + lo)] = sP[r];
+    if (frag_pending) {
+      wait_vm<1>();  // tile t + 2's copies complete (the fragment's store, issued after, need not)
+    } else {
+      wait_mem();
+    }
+    __syncthreads();  // dS complete; tile t + 2's rows landed
+
+    // The dQ partial dS K over the block's keys (the wave's dim tile w).
+    p1 = zero4();
+    if (q0 < S && wave_dq) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f4 x = ld4(&sdS[buf][swz<kBwdKeys>(lo, 16 * g + 4 * u)]);
+        p1 = mma(x.x, kQ[4 * u], p1);
+        p1 = mma(x.y, kQ[4 * u + 1], p1);
+        p1 = mma(x.z, kQ[4 * u + 2], p1);
+        p1 = mma(x.w, kQ[4 * u + 3], p1);
+      }
+    }
+    // D of tile t + 2 (its rows landed before the barrier).
+    if (t + 2 < nsteps) rowsum_do_o(Const<(buf + 2) % kNB>{});
+  };
+  // Unrolled by three, so that every LDS buffer index is a compile-time constant.
+  for (int t = 0; t < nsteps; t += 3) {
+    tile_step(Const<0>{}, t);
+    if (t + 1 < nsteps) tile_step(Const<1>{}, t + 1);
+    if (t + 2 < nsteps) tile_step(Const<2>{}, t + 2);
+  }
+  if (wave_dq) store_frag(t0 + nsteps - 1);  // the last tile's fragment
+
+  // dK (x scale) and dV of this lane's key: dims 16 mt + 4 g .. + 3, one float4 each.
+  if (key < S) {
+    float* row = a.dqkv + (static_cast<int64_t>(b) * S + key) * 3 * a.H * D +
+                 static_cast<int64_t>(h) * D;
+    const int64_t part = static_cast<int64_t>(a.H) * D;
+#pragma unroll
+    for (int mt = 0; mt < kDT; ++mt) {
+      st4(row + part + 16 * mt + 4 * g, dka[mt] * a.scale);
+      st4(row + 2 * part + 16 * mt + 4 * g, dva[mt]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Backward, step 3 (split only): dQ of one (b, h, query tile) per workgroup, the tile's partials
 // summed in key-block order, ((p_0 + p_1) + p_2) + ..., times scale (the same operations, in the
 // same order, as the turn hand-over). Float4 i of a partial (fragment order: dim tile dt = i / 64
@@ -1246,16 +1583,20 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   BwdArgs a{q, k, v, d_o, o, lse, dsum, dqkv, part, turn, ctrl, b, h, s,
             nkb, ntile, scale, causal, stagger};
   void* args[] = {&a};
+  if (split && d <= 64) {
+    const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32>)
+                             : reinterpret_cast<const void*>(bwd_split_kernel<64>);
+    return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
+  }
+  // The turn mode at every head_dim; the split mode at 128 (no LDS room for bwd_split_kernel).
   const void* fn;
   if (d == 32) {
-    fn = split ? reinterpret_cast<const void*>(bwd_kernel<true, 32>)
-               : reinterpret_cast<const void*>(bwd_kernel<false, 32>);
+    fn = reinterpret_cast<const void*>(bwd_kernel<false, 32>);
   } else if (d == 128) {
     fn = split ? reinterpret_cast<const void*>(bwd_kernel<true, 128>)
                : reinterpret_cast<const void*>(bwd_kernel<false, 128>);
   } else {
-    fn = split ? reinterpret_cast<const void*>(bwd_kernel<true, 64>)
-               : reinterpret_cast<const void*>(bwd_kernel<false, 64>);
+    fn = reinterpret_cast<const void*>(bwd_kernel<false, 64>);
   }
   return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
 }
