@@ -336,8 +336,14 @@ fwd_kernel(FwdArgs a) {
   constexpr int kDT = D / 16;              // 16-dim tiles of O
   constexpr int kCopies = KT / kCopyRows<D>;  // direct copies per K (or V) tile
   static_assert(KT % kCopyRows<D> == 0, "whole copies per tile");
-  __shared__ __attribute__((aligned(16))) float sK[2][kFwdKeys * D];
-  __shared__ __attribute__((aligned(16))) float sV[2][kFwdKeys * D];
+  // One LDS array (each tile a constant offset from one base, folded into the LDS instructions).
+  struct Smem {
+    float k[2][kFwdKeys * D], v[2][kFwdKeys * D];
+  };
+  __shared__ __attribute__((aligned(16))) Smem sm;
+  auto& sK = sm.k;
+  auto& sV = sm.v;
+  const unsigned lds0 = lds_addr(&sm);
 
   const int tid = threadIdx.x, lane = tid & 63, lo = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
@@ -385,12 +391,13 @@ fwd_kernel(FwdArgs a) {
 
   // Staging: wave w issues copies w, w + 4, ... of the K and V tiles; keys past S repeat key
   // S - 1 (finite; their scores are masked, so 0 * V stays 0).
-  auto stage = [&](int kt0, int buf) {
+  auto stage = [&](int kt0, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
 #pragma unroll
     for (int j0 = 0; j0 < kCopies; j0 += 4) {
       if (j0 + w < kCopies) {
-        copy_part<D>(kp, k_ss4, kt0, S - 1, sK[buf], j0 + w, lane);
-        copy_part<D>(vp, v_ss4, kt0, S - 1, sV[buf], j0 + w, lane);
+        copy_part_at<D>(kp, k_ss4, kt0, S - 1, lds0 + offsetof(Smem, k[buf]), j0 + w, lane);
+        copy_part_at<D>(vp, v_ss4, kt0, S - 1, lds0 + offsetof(Smem, v[buf]), j0 + w, lane);
       }
     }
   };
@@ -405,21 +412,27 @@ fwd_kernel(FwdArgs a) {
     for (int mt = 0; mt < kDT; ++mt) acc[n][mt] = zero4();
   }
 
-  stage(0, 0);
+  stage(0, Const<0>{});
   wait_mem();
   __syncthreads();
   // One key tile; unrolled by two so that the LDS buffer (t % 2) is a compile-time constant and
-  // LDS addresses fold its offset into the instruction.
-  auto tile_step = [&](auto bufc, int t) {
-    const int buf = bufc(), kt0 = t * kFwdKeys;
+  // LDS addresses fold its offset into the instruction. kFull: an interior tile of the wave
+  // (every key below S and, causal, none after the wave's first query) -- no liveness test, no
+  // mask; the masked variant serves the rest.
+  auto tile_step = [&](auto bufc, auto fullc, int t) {
+    constexpr int buf = decltype(bufc)::value;
+    constexpr bool kFull = decltype(fullc)::value != 0;
+    const int kt0 = t * kFwdKeys;
     // The next tile into the other buffer, whose last readers passed the last barrier.
-    if (t + 1 < ntiles) stage(kt0 + kFwdKeys, buf ^ 1);
-    if (wave_live) {
+    if (t + 1 < ntiles) stage(kt0 + kFwdKeys, Const<buf ^ 1>{});
+    if (kFull || wave_live) {
       const float* Kt = sK[buf];
       const float* Vt = sV[buf];
       bool live[kFwdSub];
 #pragma unroll
-      for (int mt = 0; mt < kFwdSub; ++mt) live[mt] = kt0 + 16 * mt < kw_end;  // wave-uniform
+      for (int mt = 0; mt < kFwdSub; ++mt) {
+        live[mt] = kFull || kt0 + 16 * mt < kw_end;  // wave-uniform
+      }
       f4 s[kFwdNT][kFwdSub];
 #pragma unroll
       for (int mt = 0; mt < kFwdSub; ++mt) {
@@ -443,10 +456,9 @@ fwd_kernel(FwdArgs a) {
       for (int n = 0; n < kFwdNT; ++n) {
         const int qi = qw0 + 16 * n + lo;
         // Mask (keys past S; causal keys after the query) and the tile's row max of the raw
-        // scores. Non-causal tiles whose keys are all below S (wave-uniform test) skip the mask.
+        // scores (interior tiles: no mask).
         float tmax = kNegInf;
-        const bool full = !a.causal && kt0 + kFwdKeys <= S;
-        if (full) {
+        if (kFull) {
 #pragma unroll
           for (int mt = 0; mt < kFwdSub; ++mt) {
 #pragma unroll
@@ -482,7 +494,7 @@ fwd_kernel(FwdArgs a) {
         // p = 2^(s c2 - m c2): one fma per score.
         const float mc = m[n] * c2;
         float psum = 0.0f;
-        if (full) {
+        if (kFull) {
 #pragma unroll
           for (int mt = 0; mt < kFwdSub; ++mt) {
 #pragma unroll
@@ -525,9 +537,19 @@ fwd_kernel(FwdArgs a) {
     wait_mem();       // the next tile's copies have landed
     __syncthreads();  // and every wave is done with this tile's buffers
   };
+  // Interior tiles of this wave: tiles whose keys are all below S and, causal, all at or before
+  // the wave's first query (wave-uniform).
+  const int full_end = (a.causal ? min(S, qw0 + 1) : S) / kFwdKeys;
+  auto step = [&](auto bufc, int t) {
+    if (wave_live && t < full_end) {
+      tile_step(bufc, Const<1>{}, t);
+    } else {
+      tile_step(bufc, Const<0>{}, t);
+    }
+  };
   for (int t = 0; t < ntiles; t += 2) {
-    tile_step(Const<0>{}, t);
-    if (t + 1 < ntiles) tile_step(Const<1>{}, t + 1);
+    step(Const<0>{}, t);
+    if (t + 1 < ntiles) step(Const<1>{}, t + 1);
   }
 
   if (wave_live) {
