@@ -226,7 +226,7 @@ def main() -> int:
                        "step": round(steps_us, 2)},
         "dq_sum": "split" if split else "turns",
         "roofline": {
-            "kernel": ("bwd_kernel<true, 64> (fattn_bwd_main_f32_d64, split)" if split
+            "kernel": ("bwd_split_kernel<64> (fattn_bwd_main_f32_d64, split)" if split
                        else "bwd_kernel<false, 64> (fattn_bwd_main_f32_d64, turns)"),
             "bound": "mfma",
             "achieved": round(main_tflops, 3),

@@ -69,6 +69,11 @@ __device__ __forceinline__ f4 mma(float a, float b, f4 c) {
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ __forceinline__ void st4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
+// Non-temporal store (nt): for outputs no kernel of the same pass reads again, so that they do not
+// sit dirty in the L2s when the kernel ends (each XCD's L2 writes its dirty lines back then).
+__device__ __forceinline__ void st4_nt(float* p, f4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+}
 __device__ __forceinline__ f4 zero4() { return f4{0.0f, 0.0f, 0.0f, 0.0f}; }
 
 // A lane of x through a DPP lane permutation (VALU, no LDS round trip).
@@ -565,8 +570,11 @@ fwd_kernel(FwdArgs a) {
         const float inv = 1.0f / l;
         float* orow = a.o + ((static_cast<int64_t>(b) * S + qi) * a.H + h) * D;
 #pragma unroll
-        for (int mt = 0; mt < kDT; ++mt) st4(orow + 16 * mt + 4 * g, acc[n][mt] * inv);
-        if (g == 0) a.lse[static_cast<int64_t>(bh) * S + qi] = m[n] * ascale + logf(l);
+        for (int mt = 0; mt < kDT; ++mt) st4_nt(orow + 16 * mt + 4 * g, acc[n][mt] * inv);
+        if (g == 0) {
+          __builtin_nontemporal_store(m[n] * ascale + logf(l),
+                                      a.lse + static_cast<int64_t>(bh) * S + qi);
+        }
       }
     }
   }
