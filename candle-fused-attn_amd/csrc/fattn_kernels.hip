@@ -424,9 +424,10 @@ fwd_kernel(FwdArgs a) {
   // LDS addresses fold its offset into the instruction. kFull: an interior tile of the wave
   // (every key below S and, causal, none after the wave's first query) -- no liveness test, no
   // mask; the masked variant serves the rest.
-  auto tile_step = [&](auto bufc, auto fullc, int t) {
+  auto tile_step = [&](auto bufc, auto fullc, auto colsc, int t) {
     constexpr int buf = decltype(bufc)::value;
     constexpr bool kFull = decltype(fullc)::value != 0;
+    constexpr int kCols = decltype(colsc)::value;  // column tiles with a query below S
     const int kt0 = t * kFwdKeys;
     // The next tile into the other buffer, whose last readers passed the last barrier.
     if (t + 1 < ntiles) stage(kt0 + kFwdKeys, Const<buf ^ 1>{});
@@ -448,7 +449,7 @@ fwd_kernel(FwdArgs a) {
           for (int u = 0; u < kQR / 4; ++u) {
             const f4 kk = ld4(Kt + swz<D>(16 * mt + lo, kQR * g + 4 * u));
 #pragma unroll
-            for (int n = 0; n < kFwdNT; ++n) {
+            for (int n = 0; n < kCols; ++n) {
               s[n][mt] = mma(kk.x, qr[n][4 * u], s[n][mt]);
               s[n][mt] = mma(kk.y, qr[n][4 * u + 1], s[n][mt]);
               s[n][mt] = mma(kk.z, qr[n][4 * u + 2], s[n][mt]);
@@ -458,7 +459,7 @@ fwd_kernel(FwdArgs a) {
         }
       }
 #pragma unroll
-      for (int n = 0; n < kFwdNT; ++n) {
+      for (int n = 0; n < kCols; ++n) {
         const int qi = qw0 + 16 * n + lo;
         // Mask (keys past S; causal keys after the query) and the tile's row max of the raw
         // scores (interior tiles: no mask).
@@ -534,7 +535,7 @@ fwd_kernel(FwdArgs a) {
           for (int mt = 0; mt < kDT; ++mt) {
             const float vv = Vt[swz<D>(16 * kt + 4 * g + r, 16 * mt + lo)];
 #pragma unroll
-            for (int n = 0; n < kFwdNT; ++n) acc[n][mt] = mma(vv, s[n][kt][r], acc[n][mt]);
+            for (int n = 0; n < kCols; ++n) acc[n][mt] = mma(vv, s[n][kt][r], acc[n][mt]);
           }
         }
       }
@@ -543,13 +544,19 @@ fwd_kernel(FwdArgs a) {
     __syncthreads();  // and every wave is done with this tile's buffers
   };
   // Interior tiles of this wave: tiles whose keys are all below S and, causal, all at or before
-  // the wave's first query (wave-uniform).
-  const int full_end = (a.causal ? min(S, qw0 + 1) : S) / kFwdKeys;
+  // the wave's first query (wave-uniform); none for a wave whose queries run past S. A wave with
+  // its last column tile wholly past S (two column tiles, the second dead) computes only the
+  // first.
+  const bool all_cols = qw0 + kFwdWaveQ - 16 < S;
+  const int full_end =
+      qw0 + kFwdWaveQ <= S ? (a.causal ? min(S, qw0 + 1) : S) / kFwdKeys : 0;
   auto step = [&](auto bufc, int t) {
     if (wave_live && t < full_end) {
-      tile_step(bufc, Const<1>{}, t);
+      tile_step(bufc, Const<1>{}, Const<kFwdNT>{}, t);
+    } else if (kFwdNT != 2 || all_cols) {
+      tile_step(bufc, Const<0>{}, Const<kFwdNT>{}, t);
     } else {
-      tile_step(bufc, Const<0>{}, t);
+      tile_step(bufc, Const<0>{}, Const<1>{}, t);
     }
   };
   for (int t = 0; t < ntiles; t += 2) {
@@ -1473,7 +1480,13 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
   constexpr int kF4 = kQT * D / 4;             // float4s per tile
   __shared__ __attribute__((aligned(16))) float tile[kQT * kPitch];
   const int tid = threadIdx.x;
-  const int bh = static_cast<int>(blockIdx.x) / ntile, j = static_cast<int>(blockIdx.x) % ntile;
+  // Non-causal: the tiles of a (b, h) on the XCD that ran its key blocks in step 2 (the same
+  // XCD-major split of the grid), the (b, h) written last first, whose partials are likeliest
+  // still cached.
+  const int tot = B * H * ntile;
+  int it = static_cast<int>(blockIdx.x);
+  if (!causal && it < (tot & ~7)) it = (it & 7) * (tot >> 3) + ((tot >> 3) - 1 - (it >> 3));
+  const int bh = it / ntile, j = it % ntile;
   const int b = bh / H, h = bh % H, q0 = j * kQT;
   // Contributors: causal, the key blocks holding a key <= the tile's last query.
   const int cnt = causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) + 1 : nkb;
