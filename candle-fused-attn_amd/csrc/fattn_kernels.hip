@@ -147,35 +147,53 @@ __device__ __forceinline__ void transpose_groups(f4& x0, f4& x1, f4& x2, f4& x3)
 // of lane group g reads dims 16 u + 4 g .. + 3, so the four groups' loads of one row are 64
 // contiguous bytes -- and 4 x 4 transposes across the lane groups move every float4 to its
 // quarter's group (D 64: one transpose; D 128: one over the even loads, one over the odd). At D 32
-// each lane reads its quarter directly (two float4s). Every lane of the wave must execute it.
+// each lane reads its quarter directly (two float4s). Two phases, so that a caller can issue other
+// memory operations between the loads and the transposes (which wait for the loads): quarter_issue
+// then quarter_place, or load_quarter for both. Every lane of the wave must execute them.
 template <int D>
-__device__ __forceinline__ void load_quarter(const float* row, int g, float (&dst)[D / 4]) {
+struct Quarter {
+  f4 x[D == 32 ? 2 : D / 16];
+};
+template <int D>
+__device__ __forceinline__ void quarter_issue(const float* row, int g, Quarter<D>& q) {
+  if constexpr (D == 32) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) q.x[u] = ld4(row + 8 * g + 4 * u);
+  } else {
+#pragma unroll
+    for (int u = 0; u < D / 16; ++u) q.x[u] = ld4(row + 16 * u + 4 * g);
+  }
+}
+template <int D>
+__device__ __forceinline__ void quarter_place(Quarter<D>& q, float (&dst)[D / 4]) {
   if constexpr (D == 32) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const f4 x = ld4(row + 8 * g + 4 * u);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dst[4 * u + e] = x[e];
+      for (int e = 0; e < 4; ++e) dst[4 * u + e] = q.x[u][e];
     }
   } else {
     constexpr int kU = D / 16;
-    f4 x[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) x[u] = ld4(row + 16 * u + 4 * g);
     if constexpr (D == 64) {
-      transpose_groups(x[0], x[1], x[2], x[3]);
+      transpose_groups(q.x[0], q.x[1], q.x[2], q.x[3]);
     } else {
-      transpose_groups(x[0], x[2], x[4], x[6]);
-      transpose_groups(x[1], x[3], x[5], x[7]);
+      transpose_groups(q.x[0], q.x[2], q.x[4], q.x[6]);
+      transpose_groups(q.x[1], q.x[3], q.x[5], q.x[7]);
     }
 #pragma unroll
     for (int j = 0; j < kU; ++j) {
       // D 64: x[j] holds dims 16 g + 4 j; D 128: x[2 i] dims 32 g + 4 i, x[2 i + 1] 32 g + 16 + 4 i.
       const int at = D == 64 ? 4 * j : (j % 2 == 0 ? 2 * j : 16 + 2 * (j - 1));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dst[at + e] = x[j][e];
+      for (int e = 0; e < 4; ++e) dst[at + e] = q.x[j][e];
     }
   }
+}
+template <int D>
+__device__ __forceinline__ void load_quarter(const float* row, int g, float (&dst)[D / 4]) {
+  Quarter<D> q;
+  quarter_issue<D>(row, g, q);
+  quarter_place<D>(q, dst);
 }
 
 typedef __attribute__((address_space(3))) float lds_float;
@@ -377,12 +395,10 @@ fwd_kernel(FwdArgs a) {
   // negated for a negative scale (so that the raw scores' max is the scaled scores' max).
   const float qsign = a.scale < 0.0f ? -1.0f : 1.0f;
   float qr[kFwdNT][kQR];
+  Quarter<D> qload[kFwdNT];  // placed into qr after the first key tile's copies are issued
 #pragma unroll
   for (int n = 0; n < kFwdNT; ++n) {
-    const int qi = qw0 + 16 * n + lo;
-    load_quarter<D>(qp + min(qi, S - 1) * a.q.ss, g, qr[n]);
-#pragma unroll
-    for (int t = 0; t < kQR; ++t) qr[n][t] = qi < S ? qr[n][t] * qsign : 0.0f;
+    quarter_issue<D>(qp + min(qw0 + 16 * n + lo, S - 1) * a.q.ss, g, qload[n]);
   }
 
   // Scores enter the exponent as s * c2 (c2 = |scale| log2 e); m holds raw-score maxima.
@@ -418,6 +434,13 @@ fwd_kernel(FwdArgs a) {
   }
 
   stage(0, Const<0>{});
+#pragma unroll
+  for (int n = 0; n < kFwdNT; ++n) {
+    const int qi = qw0 + 16 * n + lo;
+    quarter_place<D>(qload[n], qr[n]);
+#pragma unroll
+    for (int t = 0; t < kQR; ++t) qr[n][t] = qi < S ? qr[n][t] * qsign : 0.0f;
+  }
   wait_mem();
   __syncthreads();
   // One key tile; unrolled by two so that the LDS buffer (t % 2) is a compile-time constant and
@@ -1273,16 +1296,13 @@ bwd_split_kernel(BwdArgs a) {
 
   // K, V of this lane's key (B operands of S and dP) and kQ[t] = K[k0 + 16 g + t][16 w + lo]
   // (B operand of the dQ product), zero past S.
+  // (Loads issued here; K and V are placed after the first tiles' copies are issued, below.)
   float kB[kKR], vB[kKR], kQ[16];
+  Quarter<D> kload, vload;
   {
     const int kr = min(key, S - 1);
-    load_quarter<D>(kp + kr * a.k.ss, g, kB);
-    load_quarter<D>(vp + kr * a.v.ss, g, vB);
-#pragma unroll
-    for (int t = 0; t < kKR; ++t) {
-      kB[t] = key < S ? kB[t] : 0.0f;
-      vB[t] = key < S ? vB[t] : 0.0f;
-    }
+    quarter_issue<D>(kp + kr * a.k.ss, g, kload);
+    quarter_issue<D>(vp + kr * a.v.ss, g, vload);
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
       const int kk = k0 + 16 * g + t;
@@ -1347,6 +1367,13 @@ bwd_split_kernel(BwdArgs a) {
 
   gload(0, Const<0>{});
   if (nsteps > 1) gload(1, Const<1>{});
+  quarter_place<D>(kload, kB);
+  quarter_place<D>(vload, vB);
+#pragma unroll
+  for (int t = 0; t < kKR; ++t) {
+    kB[t] = key < S ? kB[t] : 0.0f;
+    vB[t] = key < S ? vB[t] : 0.0f;
+  }
   wait_mem();  // the direct copies have landed
   __syncthreads();
   rowsum_do_o(Const<0>{});
