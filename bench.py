@@ -159,8 +159,9 @@ def main() -> int:
     # Per-kernel durations: K more steps, back to back as above, with the backward launched as
     # its kernel-level steps (the same kernels on the same arguments as fattn_qkv_backward) and a
     # HIP event on the launch stream between every two launches.
-    # Step 1 launches nothing with a split workspace at d 64 (step 2 computes D itself).
-    kernels = [("fwd", fwd)] + ([] if split else [("bwd_prep", prep_k)]) + [("bwd_main", main_k)]
+    # With a split workspace at d 64, step 1 only clears the counters of the dQ sums that step 2's
+    # last workgroups do (step 2 computes D itself); step 3 sums the tiles those left.
+    kernels = [("fwd", fwd), ("bwd_prep", prep_k), ("bwd_main", main_k)]
     if split:
         kernels.append(("bwd_dq", dq_k))
     marks = []
@@ -185,6 +186,7 @@ def main() -> int:
     fwd_tflops = f_fwd / (fwd_ms * 1e-3) / 1e12
     total_tflops = (f_fwd + f_bwd) / (fwd_bwd_ms * 1e-3) / 1e12
     main_tflops = f_bwd / (main_us * 1e-6) / 1e12
+    bwd_steps_tflops = f_bwd / ((prep_us + main_us + dq_us) * 1e-6) / 1e12
     fwdk_tflops = f_fwd / (fwd_us * 1e-6) / 1e12
 
     traffic = None
@@ -226,7 +228,8 @@ def main() -> int:
                        "step": round(steps_us, 2)},
         "dq_sum": "split" if split else "turns",
         "roofline": {
-            "kernel": ("bwd_split_kernel<64> (fattn_bwd_main_f32_d64, split)" if split
+            "kernel": ("bwd_split_kernel<64> (fattn_bwd_main_f32_d64, split; its last "
+                       "workgroups sum dQ tiles)" if split
                        else "bwd_kernel<false, 64> (fattn_bwd_main_f32_d64, turns)"),
             "bound": "mfma",
             "achieved": round(main_tflops, 3),
@@ -235,6 +238,7 @@ def main() -> int:
             "frac": round(main_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             "traffic": traffic,
             "flops_per_launch": f_bwd,
+            "bwd_steps_1_3_achieved": round(bwd_steps_tflops, 3),
             "fwd_kernel_achieved": round(fwdk_tflops, 3),
             "fwd_kernel_frac": round(fwdk_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
         },

@@ -25,8 +25,10 @@ Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d) {
   w.ctrl_off = w.turn_off + up(tiles * sizeof(int));
   w.part_off = w.ctrl_off + up(64 * sizeof(int));
   w.bytes_min = w.part_off;
-  w.bytes_split = w.part_off + up(nkb * tiles * kBwdQueryTile * static_cast<size_t>(d) *
-                                  sizeof(float));
+  w.arrive_off = w.part_off + up(nkb * tiles * kBwdQueryTile * static_cast<size_t>(d) *
+                                 sizeof(float));
+  w.done_off = w.arrive_off + up(static_cast<size_t>(b * h) * sizeof(unsigned long long));
+  w.bytes_split = w.done_off + up(tiles * sizeof(unsigned));
   return w;
 }
 
@@ -78,8 +80,8 @@ int check_range(const char* who, int64_t b, int64_t h, int64_t s, int64_t d) {
   const int dd = static_cast<int>(d);
   if (fattn::forward_blocks(b, h, s, 1, dd) > grid_lim ||
       fattn::forward_blocks(b, h, s, 0, dd) > grid_lim ||
-      fattn::bwd_main_blocks(b, h, s) > grid_lim || fattn::bwd_prep_blocks(b, h, s, dd) > grid_lim ||
-      fattn::bwd_dq_blocks(b, h, s) > grid_lim) {
+      fattn::bwd_main_blocks(b, h, s) + fattn::bwd_dq_blocks(b, h, s) + 8 > grid_lim ||
+      fattn::bwd_prep_blocks(b, h, s, dd) > grid_lim) {
     return fail(FATTN_ERANGE, std::string(who) + ": the grid for " + std::to_string(b) +
                                   " x " + std::to_string(h) + " x " + std::to_string(s) +
                                   " exceeds the launch limit");
@@ -145,6 +147,8 @@ int run_forward(const char* who, View q, View k, View v, float* o, float* lse, i
 struct WsParts {
   float* dsum;
   float* part;  // null: the workspace is too small for the split partials (turn hand-over)
+  unsigned long long* arrive;  // split: step 2's dQ sums
+  unsigned* done;
   int* turn;
   int* ctrl;
 };
@@ -160,13 +164,18 @@ int workspace_parts(const char* who, void* ws, size_t ws_bytes, int64_t b, int64
   char* base = static_cast<char*>(ws);
   out->dsum = reinterpret_cast<float*>(base + l.d_off);
   out->part = ws_bytes >= l.bytes_split ? reinterpret_cast<float*>(base + l.part_off) : nullptr;
+  out->arrive =
+      out->part ? reinterpret_cast<unsigned long long*>(base + l.arrive_off) : nullptr;
+  out->done = out->part ? reinterpret_cast<unsigned*>(base + l.done_off) : nullptr;
   out->turn = reinterpret_cast<int*>(base + l.turn_off);
   out->ctrl = reinterpret_cast<int*>(base + l.ctrl_off);
   return 0;
 }
 
+// causal: -1 when unknown (the step-level entry), which clears the counters of step 2's dQ sums
+// whenever they may be used.
 int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_bytes, int64_t b,
-                 int64_t h, int64_t s, int64_t d, void* stream) {
+                 int64_t h, int64_t s, int64_t d, int causal, void* stream) {
   if (int rc = check_range(who, b, h, s, d)) return rc;
   if (!o || !d_o.p) return fail(FATTN_EINVAL, std::string(who) + ": null operand");
   if (!aligned16(o) || !view_aligned(d_o)) {
@@ -174,11 +183,16 @@ int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_
   }
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
-  // split (d <= 64): step 2 computes D itself and needs no counters.
-  if (!fattn::bwd_needs_prep(p.part != nullptr, static_cast<int>(d))) return ok();
-  const int err = fattn::launch_bwd_prep(o, d_o, p.dsum, p.turn, p.ctrl, static_cast<int>(b),
-                                         static_cast<int>(h), static_cast<int>(s),
-                                         static_cast<int>(d), stream);
+  // split (d <= 64): step 2 computes D itself; step 1 zeroes the counters of its dQ sums.
+  int err = 0;
+  if (fattn::bwd_needs_prep(p.part != nullptr, static_cast<int>(d))) {
+    err = fattn::launch_bwd_prep(o, d_o, p.dsum, p.turn, p.ctrl, static_cast<int>(b),
+                                 static_cast<int>(h), static_cast<int>(s), static_cast<int>(d),
+                                 stream);
+  } else if (causal < 0 || fattn::bwd_sum_blocks(b, h, s, static_cast<int>(d), causal) > 0) {
+    const int64_t tiles = b * h * ((s + fattn::kBwdQueryTile - 1) / fattn::kBwdQueryTile);
+    err = fattn::launch_bwd_clear(p.arrive, b * h, p.done, tiles, stream);
+  }
   if (err) return hip_fail(err, "backward step 1 launch");
   return ok();
 }
@@ -187,7 +201,8 @@ int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d
                  const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
                  int64_t s, int64_t d, float scale, int causal, void* stream) {
   if (int rc = check_range(who, b, h, s, d)) return rc;
-  if (!slice_fits(q, s, d) || !slice_fits(d_o, s, d) || s * 3 * h * d > int64_t{UINT32_MAX}) {
+  if (!slice_fits(q, s, d) || !slice_fits(k, s, d) || !slice_fits(v, s, d) ||
+      !slice_fits(d_o, s, d) || s * 3 * h * d > int64_t{UINT32_MAX}) {
     return slice_error(who, s);
   }
   if (!q.p || !k.p || !v.p || !o || !d_o.p || !lse || !dqkv) {
@@ -199,8 +214,9 @@ int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d
   }
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
-  const int err = fattn::launch_bwd_main(q, k, v, d_o, o, lse, p.dsum, dqkv, p.part, p.turn, p.ctrl,
-                                         static_cast<int>(b), static_cast<int>(h),
+  const int err = fattn::launch_bwd_main(q, k, v, d_o, o, lse, p.dsum, dqkv, p.part, p.arrive,
+                                         p.done, p.turn, p.ctrl, static_cast<int>(b),
+                                         static_cast<int>(h),
                                          static_cast<int>(s), static_cast<int>(d), scale,
                                          causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 2 launch");
@@ -219,9 +235,9 @@ int run_bwd_dq(const char* who, float* dqkv, void* ws, size_t ws_bytes, int64_t 
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
   if (!p.part) return ok();
-  const int err = fattn::launch_bwd_dq(p.part, dqkv, static_cast<int>(b), static_cast<int>(h),
-                                       static_cast<int>(s), static_cast<int>(d), scale,
-                                       causal ? 1 : 0, stream);
+  const int err = fattn::launch_bwd_dq(p.part, p.done, dqkv, static_cast<int>(b),
+                                       static_cast<int>(h), static_cast<int>(s),
+                                       static_cast<int>(d), scale, causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 3 launch");
   return ok();
 }
@@ -229,7 +245,9 @@ int run_bwd_dq(const char* who, float* dqkv, void* ws, size_t ws_bytes, int64_t 
 int run_backward(const char* who, View q, View k, View v, const float* o, View d_o,
                  const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
                  int64_t s, int64_t d, float scale, int causal, void* stream) {
-  if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, d, stream)) return rc;
+  if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, d, causal ? 1 : 0, stream)) {
+    return rc;
+  }
   if (int rc = run_bwd_main(who, q, k, v, o, d_o, lse, dqkv, ws, ws_bytes, b, h, s, d, scale,
                             causal, stream)) {
     return rc;
@@ -343,7 +361,7 @@ int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_stride
   if (empty3(b, h, s)) return ok();
   if (!do_strides) return fail(FATTN_EINVAL, "fused_attention: null strides");
   return run_bwd_prep("fused_attention", o, make_view(d_o, do_strides), workspace,
-                      workspace_bytes, b, h, s, d, stream);
+                      workspace_bytes, b, h, s, d, -1, stream);
 }
 
 int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* o,

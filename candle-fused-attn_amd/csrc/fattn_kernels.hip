@@ -687,6 +687,12 @@ struct BwdArgs {
   const float* dsum;  // otherwise: D from step 1
   float* dqkv;
   float* part;  // split: the dQ partials, [nkb][b h][ntile][kQT * D] in fragment order
+  // split, D <= 64, null when step 3 sums every tile: key blocks finished per (b, h) (byte x
+  // counts those on XCD x) and the flags of the tiles summed here. Workgroups from n_main on sum
+  // tiles; n_main (the key blocks, rounded up to a multiple of 8) and the sums' layout below.
+  unsigned long long* arrive;
+  unsigned* done;
+  int n_main;
   int* turn;
   int* ctrl;
   int B, H, S, nkb, ntile;
@@ -1238,6 +1244,84 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // folds such offsets into the LDS instructions, where across separate arrays it keeps an address
 // register per array (at D 64 that saves 24 registers).
 // ---------------------------------------------------------------------------------------------
+// dQ sums inside step 2 (split, non-causal, D <= 64). Step 3 moves 118 MB at config 2 after step
+// 2's tail, where the CUs run fewer and fewer key blocks; workgroups appended to step 2's grid do
+// its sums in that tail instead. In-order dispatch starts them only once every key block has been
+// dispatched. Workgroup n_main + 8 m + x (on XCD x: workgroups go to the XCDs round robin on
+// MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks xcd_remap puts on XCD x:
+// `per` consecutive (b, h)s from x per (the host enables this only when per is whole), kSumTiles
+// tiles per chunk, in the order their key blocks were dispatched. Thread 0 polls the (b, h)'s
+// counter -- an atomic add of 0, at the same coherence point as the key blocks' additions -- until
+// every key block has counted itself (each does so once its partials are stored), sleeping between
+// polls, giving up after kSumPolls. The chunk is summed only if every key block counted itself on
+// this workgroup's XCD: all partials are then in this XCD's L2 (or written back from it). The sum
+// is step 3's, operation for operation: float4 i of a tile's partials in key-block order, times
+// scale (so the results are bit-identical whichever kernel sums a tile), stored from fragment
+// order straight into dQ rows (16 lanes write 64 contiguous bytes). Then the chunk's done flags;
+// step 3 sums the tiles without one, so a key block on another XCD, or a poll that gave up, only
+// leaves work to step 3. Every poll ends: the key blocks have smaller workgroup numbers on the same
+// XCD, so they were dispatched before this workgroup and run to completion whatever it does.
+constexpr int kSumPolls = 4096;
+constexpr int kSumTiles = 3;  // query tiles per summing workgroup (config 2: 1, 2, 15 slower; 4 same)
+template <int D>
+__device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, unsigned* flag) {
+  constexpr int kDT = D / 16, kF4 = kQT * D / 4;
+  const int tid = threadIdx.x, BH = a.B * a.H, ntile = a.ntile, nkb = a.nkb;
+  const int nchunk = (ntile + kSumTiles - 1) / kSumTiles;
+  const int per = ((a.n_main & ~7) >> 3) / nkb;
+  if (m >= per * nchunk) return;
+  const int bh = x * per + m / nchunk;
+  const int j0 = (m % nchunk) * kSumTiles, j1 = min(ntile, j0 + kSumTiles);
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  const unsigned long long mine = static_cast<unsigned long long>(nkb) << (8 * (xcc & 7u));
+  if (tid == 0) {
+    unsigned long long v = 0;
+    for (int it = 0; it < kSumPolls; ++it) {
+      v = __hip_atomic_fetch_add(a.arrive + bh, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // Sum of the bytes (each below 128): key blocks finished on any XCD.
+      if (static_cast<int>((v * 0x0101010101010101ull) >> 56) >= nkb) break;
+      __builtin_amdgcn_s_sleep(16);  // about 1000 cycles between polls
+    }
+    *flag = v == mine ? 1u : 0u;
+  }
+  __syncthreads();
+  if (*flag == 0u) return;
+  const int b = bh / a.H, h = bh % a.H, S = a.S;
+  const int64_t slot = static_cast<int64_t>(BH) * ntile * (kQT * D);
+  const int64_t row_stride = static_cast<int64_t>(3) * a.H * D;
+  float* const dq_bh =
+      a.dqkv + static_cast<int64_t>(b) * S * row_stride + static_cast<int64_t>(h) * D;
+  for (int j = j0; j < j1; ++j) {
+    const int q0 = j * kQT;
+    const float* src = a.part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D);
+#pragma unroll
+    for (int i = tid; i < kF4; i += kThreads) {
+      f4 acc = ld4(src + 4 * i);
+      int kb = 1;
+      for (; kb + 3 < nkb; kb += 4) {
+        const f4 x0 = ld4(src + kb * slot + 4 * i), x1 = ld4(src + (kb + 1) * slot + 4 * i);
+        const f4 x2 = ld4(src + (kb + 2) * slot + 4 * i), x3 = ld4(src + (kb + 3) * slot + 4 * i);
+        acc += x0;
+        acc += x1;
+        acc += x2;
+        acc += x3;
+      }
+      for (; kb < nkb; ++kb) acc += ld4(src + kb * slot + 4 * i);
+      acc *= a.scale;
+      // Fragment order: register r of float4 i is query q0 + 16 mm + 4 g + r, dim 16 dt + lo.
+      const int lane = i & 63, md = i >> 6, dt = md % kDT, mm = md / kDT;
+      const int lo = lane & 15, g = lane >> 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int q = q0 + 16 * mm + 4 * g + r;
+        if (q < S) dq_bh[q * row_stride + 16 * dt + lo] = acc[r];
+      }
+    }
+  }
+  if (tid < j1 - j0) a.done[static_cast<int64_t>(bh) * ntile + j0 + tid] = 1u;
+}
+
 template <int D>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BWD_WAVES)))
 bwd_split_kernel(BwdArgs a) {
@@ -1252,6 +1336,7 @@ bwd_split_kernel(BwdArgs a) {
     Tile q[kNB], g[kNB], o[kNB];
     float ds[kNB][kQT * kBwdKeys];
     float l[kNB][kQT], d[kNB][kQT];
+    unsigned flag;  // a dQ sum's poll result, from thread 0 to the workgroup
   };
   __shared__ __attribute__((aligned(16))) Smem sm;
   auto& sQ = sm.q;
@@ -1266,6 +1351,11 @@ bwd_split_kernel(BwdArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
   const int BH = a.B * a.H, S = a.S;
   const int id = static_cast<int>(blockIdx.x);
+  if (a.arrive != nullptr && id >= a.nkb * BH) {
+    // A dQ sum (the grid's last workgroups; those below n_main pad it to a multiple of 8).
+    if (id >= a.n_main) bwd_sum_tiles<D>(a, id & 7, (id - a.n_main) >> 3, &sm.flag);
+    return;
+  }
   const bool wave_dq = w < kDT;  // the wave computes dQ tiles (all waves but 2, 3 at D 32)
   // No turn waits here: the guard word reads 0.
   if (id == 0 && tid == 0) a.ctrl[kCtrlGuard] = 0;
@@ -1274,7 +1364,7 @@ bwd_split_kernel(BwdArgs a) {
   // read the same Q and dO tiles at about the same time); causal, key-block-major round-robin over
   // the XCDs (the expensive low blocks start first, spread evenly). Its walk: non-causal every
   // query tile, causal from the tile of the block's first key on.
-  const int item = a.causal ? id : xcd_remap(id, static_cast<int>(gridDim.x));
+  const int item = a.causal ? id : xcd_remap(id, a.nkb * BH);
   const int bh = a.causal ? item % BH : item / a.nkb;
   const int kb = a.causal ? item / BH : item % a.nkb;
   const int b = bh / a.H, h = bh % a.H;
@@ -1476,6 +1566,19 @@ bwd_split_kernel(BwdArgs a) {
     if (t + 2 < nsteps) tile_step(Const<2>{}, t + 2);
   }
   if (wave_dq) store_frag(t0 + nsteps - 1);  // the last tile's fragment
+  if (a.arrive != nullptr) {
+    // Every partial of this key block is stored once the stores of every wave have completed:
+    // count the block, in the byte of the XCD it runs on (dK and dV, stored below, are not read
+    // by the sums).
+    wait_mem();
+    __syncthreads();
+    if (tid == 0) {
+      unsigned xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      __hip_atomic_fetch_add(a.arrive + bh, 1ull << (8 * (xcc & 7u)), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 
   // dK (x scale) and dV of this lane's key: dims 16 mt + 4 g .. + 3, one float4 each.
   if (key < S) {
@@ -1500,6 +1603,7 @@ bwd_split_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------------------------
 template <int D>
 __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ part,
+                                                     const unsigned* __restrict__ done,
                                                      float* __restrict__ dqkv, int B, int H,
                                                      int S, int nkb, int ntile, float scale,
                                                      int causal) {
@@ -1514,6 +1618,8 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
   int it = static_cast<int>(blockIdx.x);
   if (!causal && it < (tot & ~7)) it = (it & 7) * (tot >> 3) + ((tot >> 3) - 1 - (it >> 3));
   const int bh = it / ntile, j = it % ntile;
+  // Tiles step 2 summed are done.
+  if (done != nullptr && done[static_cast<int64_t>(bh) * ntile + j] != 0u) return;
   const int b = bh / H, h = bh % H, q0 = j * kQT;
   // Contributors: causal, the key blocks holding a key <= the tile's last query.
   const int cnt = causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) + 1 : nkb;
@@ -1549,6 +1655,16 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
           ld4(&tile[row * kPitch + 4 * c4]));
     }
   }
+}
+
+// Backward, step 1 of the split mode at D <= 64 (step 2 forms D itself): zero the counters and
+// done flags of step 2's dQ sums.
+__global__ void __launch_bounds__(kThreads) clear_kernel(unsigned long long* __restrict__ arrive,
+                                                         int64_t n64, unsigned* __restrict__ done,
+                                                         int64_t n32) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < n64) arrive[i] = 0ull;
+  if (i < n32) done[i] = 0u;
 }
 
 }  // namespace
@@ -1621,6 +1737,24 @@ int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d) {
 }
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQT - 1) / kQT); }
 bool bwd_needs_prep(bool split, int d) { return !split || d > 64; }
+int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  const int64_t nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT, bh = b * h;
+  // Causal: every (b, h) finishes near the end of step 2 (its key blocks are spread over the whole
+  // key-block-major order), so its sums would only lengthen the kernel (config 3: +4 %).
+  if (causal || d > 64 || nkb > kSumMaxBlocks) return 0;
+  const int64_t nchunk = (ntile + kSumTiles - 1) / kSumTiles;
+  // Non-causal: XCD x holds key blocks [x F, (x + 1) F) of the (b h)-major order, F = full / 8.
+  const int64_t f = ((nkb * bh) & ~int64_t{7}) / 8;
+  return f % nkb == 0 && f > 0 ? 8 * (f / nkb) * nchunk : 0;
+}
+
+int launch_bwd_clear(unsigned long long* arrive, int64_t n64, unsigned* done, int64_t n32,
+                     void* stream) {
+  void* args[] = {&arrive, &n64, &done, &n32};
+  const int64_t n = n64 > n32 ? n64 : n32;
+  return static_cast<int>(launch(reinterpret_cast<const void*>(clear_kernel),
+                                 (n + kThreads - 1) / kThreads, args, stream));
+}
 
 int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s, int d,
                    float scale, int causal, void* stream) {
@@ -1645,18 +1779,23 @@ int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl,
 }
 
 int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const float* lse,
-                    const float* dsum, float* dqkv, float* part, int* turn, int* ctrl, int b,
-                    int h, int s, int d, float scale, int causal, void* stream) {
+                    const float* dsum, float* dqkv, float* part, unsigned long long* arrive,
+                    unsigned* done, int* turn, int* ctrl, int b, int h, int s, int d,
+                    float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
   const bool split = part != nullptr;
   const int stagger = !split && !causal && nkb <= kStaggerMaxBlocks ? 1 : 0;
-  BwdArgs a{q, k, v, d_o, o, lse, dsum, dqkv, part, turn, ctrl, b, h, s,
-            nkb, ntile, scale, causal, stagger};
+  const int64_t nsum = split ? bwd_sum_blocks(b, h, s, d, causal) : 0;
+  const int64_t nmain = (bwd_main_blocks(b, h, s) + 7) & ~int64_t{7};
+  if (nsum == 0) arrive = nullptr, done = nullptr;
+  BwdArgs a{q, k, v, d_o, o, lse, dsum, dqkv, part, arrive, done, static_cast<int>(nmain),
+            turn, ctrl, b, h, s, nkb, ntile, scale, causal, stagger};
   void* args[] = {&a};
   if (split && d <= 64) {
     const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32>)
                              : reinterpret_cast<const void*>(bwd_split_kernel<64>);
-    return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
+    return static_cast<int>(
+        launch(fn, nsum ? nmain + nsum : bwd_main_blocks(b, h, s), args, stream));
   }
   // The turn mode at every head_dim; the split mode at 128 (no LDS room for bwd_split_kernel).
   const void* fn;
@@ -1671,10 +1810,11 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
 }
 
-int launch_bwd_dq(const float* part, float* dqkv, int b, int h, int s, int d, float scale,
-                  int causal, void* stream) {
+int launch_bwd_dq(const float* part, const unsigned* done, float* dqkv, int b, int h, int s,
+                  int d, float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
-  void* args[] = {&part, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
+  if (bwd_sum_blocks(b, h, s, d, causal) == 0) done = nullptr;
+  void* args[] = {&part, &done, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
   const void* fn = d == 32    ? reinterpret_cast<const void*>(dq_kernel<32>)
                    : d == 128 ? reinterpret_cast<const void*>(dq_kernel<128>)
                               : reinterpret_cast<const void*>(dq_kernel<64>);

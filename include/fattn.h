@@ -69,8 +69,9 @@ int fattn_fwd_f32(const float* q, const float* k, const float* v, float* o, floa
 /* Backward workspace (256-byte aligned). Replaces the temporaries cuda::backward allocates
  * (dsum and turn, src/cuda.rs:200-209). Its size picks how dQ is summed over key blocks:
  *   >= fattn_bwd_workspace_split_bytes: "split" -- every key block writes its dQ partials to the
- *      workspace (about s * s * b * h * d / 16 bytes) and a third kernel sums them in key-block
- *      order; no workgroup waits on another (the faster way);
+ *      workspace (about s * s * b * h * d / 16 bytes); they are summed in key-block order by the
+ *      last workgroups of step 2 (which wait, boundedly, only for key blocks dispatched before
+ *      them) or by a third kernel; no key block waits on another (the faster way);
  *   >= fattn_bwd_workspace_min_bytes (below split): "turns" -- key blocks add into dQ in place,
  *      in key-block order, under per-query-tile turn counters; D, counters and ticket only.
  * Both are deterministic. fattn_bwd_workspace_bytes is the split size when that is at most
@@ -83,20 +84,21 @@ size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s, int64_t 
 
 /* Backward step 1: D[b, h, i] = sum_c dO[b, i, h, c] * O[b, i, h, c] (fixed order) and the
  * counters of step 2 cleared. O is [b, s, h, d] contiguous; dO is read through do_strides. With
- * a split-size workspace there is nothing to do (step 2 computes D itself; returns 0 after the
- * checks; d 128 still needs this step). Replaces the fattn_bwd_dot_f32_d64 launch
- * (src/cuda.rs:215-231). */
+ * a split-size workspace at d <= 64 step 2 computes D itself, and this step only clears the
+ * counters of the dQ sums step 2's last workgroups do. It must run before step 2 on the same
+ * workspace, in every mode. Replaces the fattn_bwd_dot_f32_d64 launch (src/cuda.rs:215-231),
+ * which also clears counters. */
 int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_strides[3],
                        void* workspace, size_t workspace_bytes, int64_t b, int64_t h, int64_t s,
                        int64_t d, void* stream);
 
 /* Backward step 2: dK and dV into ONE [b, s, 3, h, d] buffer (the fused qkv projection's
  * gradient layout); dQ summed over key blocks in a fixed order, so every rerun is bit-identical:
- * with a split-size workspace its partials go to the workspace (step 3 finishes dQ) and, for
- * d <= 64, D is computed here from O (the forward's [b, s, h, d] output); else dQ is complete
- * after this step. Where D is not computed here it comes from step 1, which must run first on
- * the same workspace (running step 1 first is always correct). Replaces the
- * fattn_bwd_f32_d64 launch (src/cuda.rs:233-258), which takes no O. */
+ * with a split-size workspace its partials go to the workspace (this step sums some query
+ * tiles, step 3 the rest) and, for d <= 64, D is computed here from O (the forward's
+ * [b, s, h, d] output); else dQ is complete after this step. Step 1 must run first on the same
+ * workspace (it clears the counters, or computes D). Replaces the fattn_bwd_f32_d64 launch
+ * (src/cuda.rs:233-258), which takes no O. */
 int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* o,
                        const float* d_o, const float* lse, float* dqkv, void* workspace,
                        size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
@@ -105,8 +107,11 @@ int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const flo
                        const int64_t do_strides[3], void* stream);
 
 /* Backward step 3: with a split-size workspace, dQ = scale * (sum of step 2's partials in
- * key-block order) into part 0 of dqkv; with a smaller one nothing to do (returns 0). Has no
- * counterpart launch in the reference (its dQ is summed in place, as the turn mode here). */
+ * key-block order) into part 0 of dqkv, for every query tile step 2 did not sum itself (its last
+ * workgroups sum the tiles of (b, h)s whose key blocks all ran on their XCD; non-causal, d <= 64;
+ * the same operations in the same order, so the result does not depend on which kernel summed a
+ * tile); with a smaller workspace nothing to do (returns 0). Has no counterpart launch in the
+ * reference (its dQ is summed in place, as the turn mode here). */
 int fattn_bwd_dq_f32(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                      int64_t s, int64_t d, float scale, int causal, void* stream);
 

@@ -490,6 +490,32 @@ def test_split_and_turns_agree(orc, cuda, causal):
             assert rel <= 1e-6
 
 
+@pytest.mark.parametrize("h,s", [(9, 240), (9, 100), (17, 50)])
+def test_dq_sums_in_step2_match_step3(orc, cuda, h, s):
+    """Non-causal split backward: the last workgroups of step 2 sum the dQ tiles of the (b, h)s
+    whose key blocks an XCD ran (with workgroups dealt to the XCDs round robin, here heads
+    0-7, or 0-15 at s 50), step 3 the rest (head 8, or 16): the same operations in the same order.
+    With every head given the same q, k, v and output gradient, every head's O, dQ, dK and dV must
+    be bit-identical, whichever kernel summed it; head 0 is checked against the fp64 oracle."""
+    rng = np.random.default_rng(11)
+    one = rng.standard_normal((1, s, 3, 1, 64)).astype(np.float32)
+    x = np.ascontiguousarray(np.broadcast_to(one, (1, s, 3, h, 64))).reshape(1, s, 3 * h * 64)
+    w1 = rng.standard_normal((1, s, 1, 64)).astype(np.float32)
+    w = np.ascontiguousarray(np.broadcast_to(w1, (1, s, h, 64))).reshape(1, s, h * 64)
+    say(f"dq sums b1 h{h} s{s}")
+    out, grad = run("fused_qkv", torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), h, 64,
+                    False, 0.125)
+    o = out.reshape(1, s, h, 64)
+    g = grad.reshape(1, s, 3, h, 64)
+    for i in range(1, h):
+        assert torch.equal(bits(o[:, :, i]), bits(o[:, :, 0])), f"O of head {i}"
+        assert torch.equal(bits(g[:, :, :, i]), bits(g[:, :, :, 0])), f"gradient of head {i}"
+    ref_out, _, ref_grad = oracle_qkv(orc, one.reshape(1, s, 3 * 64), w1.reshape(1, s, 64), 1, 64,
+                                      False, np.float64, 0.125)
+    check_errors(orc, o[:, :, 0].contiguous(), g[:, :, :, 0].reshape(1, s, 3 * 64), ref_out,
+                 ref_grad, "head 0")
+
+
 # --- head_dim 32 and 128 (the reference's roadmap, ROADMAP.md:76-79) ------------------------
 
 @pytest.mark.parametrize("d", [32, 128])
