@@ -4,8 +4,11 @@
 // Validation runs before any HIP call, so a rejected call touches no device and needs none.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <chrono>
 #include <cstdint>
 #include <climits>
+#include <random>
 #include <cstdio>
 #include <string>
 
@@ -27,8 +30,9 @@ Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d) {
   w.bytes_min = w.part_off;
   w.arrive_off = w.part_off + up(nkb * tiles * kBwdQueryTile * static_cast<size_t>(d) *
                                  sizeof(float));
-  w.done_off = w.arrive_off + up(static_cast<size_t>(b * h) * sizeof(unsigned long long));
-  w.bytes_split = w.done_off + up(tiles * sizeof(unsigned));
+  w.done_off = w.arrive_off + up(static_cast<size_t>(b * h) * nkb * sizeof(unsigned long long));
+  w.epoch_off = w.done_off + up(tiles * sizeof(unsigned long long));
+  w.bytes_split = w.epoch_off + 256;
   return w;
 }
 
@@ -39,6 +43,20 @@ namespace {
 using fattn::View;
 
 thread_local std::string g_error;
+
+// A 64-bit value unique to each step 2 launch of this process (low 3 bits zero, for the XCD), the
+// sequence starting at a random point: step 2's dQ sums tag their workspace state with it.
+unsigned long long next_epoch() {
+  static std::atomic<unsigned long long> counter{[] {
+    std::random_device rd;
+    return (static_cast<unsigned long long>(rd()) << 32) ^ rd() ^
+           static_cast<unsigned long long>(
+               std::chrono::steady_clock::now().time_since_epoch().count());
+  }()};
+  unsigned long long e = 0;
+  while (e == 0) e = counter.fetch_add(1, std::memory_order_relaxed) << 3;
+  return e;
+}
 
 int fail(int code, const std::string& msg) {
   g_error = msg;
@@ -148,7 +166,8 @@ struct WsParts {
   float* dsum;
   float* part;  // null: the workspace is too small for the split partials (turn hand-over)
   unsigned long long* arrive;  // split: step 2's dQ sums
-  unsigned* done;
+  unsigned long long* done;
+  unsigned long long* epoch;
   int* turn;
   int* ctrl;
 };
@@ -166,16 +185,15 @@ int workspace_parts(const char* who, void* ws, size_t ws_bytes, int64_t b, int64
   out->part = ws_bytes >= l.bytes_split ? reinterpret_cast<float*>(base + l.part_off) : nullptr;
   out->arrive =
       out->part ? reinterpret_cast<unsigned long long*>(base + l.arrive_off) : nullptr;
-  out->done = out->part ? reinterpret_cast<unsigned*>(base + l.done_off) : nullptr;
+  out->done = out->part ? reinterpret_cast<unsigned long long*>(base + l.done_off) : nullptr;
+  out->epoch = out->part ? reinterpret_cast<unsigned long long*>(base + l.epoch_off) : nullptr;
   out->turn = reinterpret_cast<int*>(base + l.turn_off);
   out->ctrl = reinterpret_cast<int*>(base + l.ctrl_off);
   return 0;
 }
 
-// causal: -1 when unknown (the step-level entry), which clears the counters of step 2's dQ sums
-// whenever they may be used.
 int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_bytes, int64_t b,
-                 int64_t h, int64_t s, int64_t d, int causal, void* stream) {
+                 int64_t h, int64_t s, int64_t d, void* stream) {
   if (int rc = check_range(who, b, h, s, d)) return rc;
   if (!o || !d_o.p) return fail(FATTN_EINVAL, std::string(who) + ": null operand");
   if (!aligned16(o) || !view_aligned(d_o)) {
@@ -183,16 +201,11 @@ int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_
   }
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
-  // split (d <= 64): step 2 computes D itself; step 1 zeroes the counters of its dQ sums.
-  int err = 0;
-  if (fattn::bwd_needs_prep(p.part != nullptr, static_cast<int>(d))) {
-    err = fattn::launch_bwd_prep(o, d_o, p.dsum, p.turn, p.ctrl, static_cast<int>(b),
-                                 static_cast<int>(h), static_cast<int>(s), static_cast<int>(d),
-                                 stream);
-  } else if (causal < 0 || fattn::bwd_sum_blocks(b, h, s, static_cast<int>(d), causal) > 0) {
-    const int64_t tiles = b * h * ((s + fattn::kBwdQueryTile - 1) / fattn::kBwdQueryTile);
-    err = fattn::launch_bwd_clear(p.arrive, b * h, p.done, tiles, stream);
-  }
+  // split (d <= 64): step 2 computes D itself and its dQ sums need no clearing (epochs).
+  if (!fattn::bwd_needs_prep(p.part != nullptr, static_cast<int>(d))) return ok();
+  const int err = fattn::launch_bwd_prep(o, d_o, p.dsum, p.turn, p.ctrl, static_cast<int>(b),
+                                         static_cast<int>(h), static_cast<int>(s),
+                                         static_cast<int>(d), stream);
   if (err) return hip_fail(err, "backward step 1 launch");
   return ok();
 }
@@ -215,8 +228,8 @@ int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
   const int err = fattn::launch_bwd_main(q, k, v, d_o, o, lse, p.dsum, dqkv, p.part, p.arrive,
-                                         p.done, p.turn, p.ctrl, static_cast<int>(b),
-                                         static_cast<int>(h),
+                                         p.done, p.epoch, next_epoch(), p.turn, p.ctrl,
+                                         static_cast<int>(b), static_cast<int>(h),
                                          static_cast<int>(s), static_cast<int>(d), scale,
                                          causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 2 launch");
@@ -235,7 +248,7 @@ int run_bwd_dq(const char* who, float* dqkv, void* ws, size_t ws_bytes, int64_t 
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
   if (!p.part) return ok();
-  const int err = fattn::launch_bwd_dq(p.part, p.done, dqkv, static_cast<int>(b),
+  const int err = fattn::launch_bwd_dq(p.part, p.done, p.epoch, dqkv, static_cast<int>(b),
                                        static_cast<int>(h), static_cast<int>(s),
                                        static_cast<int>(d), scale, causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 3 launch");
@@ -245,9 +258,7 @@ int run_bwd_dq(const char* who, float* dqkv, void* ws, size_t ws_bytes, int64_t 
 int run_backward(const char* who, View q, View k, View v, const float* o, View d_o,
                  const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
                  int64_t s, int64_t d, float scale, int causal, void* stream) {
-  if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, d, causal ? 1 : 0, stream)) {
-    return rc;
-  }
+  if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, d, stream)) return rc;
   if (int rc = run_bwd_main(who, q, k, v, o, d_o, lse, dqkv, ws, ws_bytes, b, h, s, d, scale,
                             causal, stream)) {
     return rc;
@@ -361,7 +372,7 @@ int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_stride
   if (empty3(b, h, s)) return ok();
   if (!do_strides) return fail(FATTN_EINVAL, "fused_attention: null strides");
   return run_bwd_prep("fused_attention", o, make_view(d_o, do_strides), workspace,
-                      workspace_bytes, b, h, s, d, -1, stream);
+                      workspace_bytes, b, h, s, d, stream);
 }
 
 int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* o,

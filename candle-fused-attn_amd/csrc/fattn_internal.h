@@ -33,12 +33,15 @@ struct View {
 //   turn   [b, h, ntile] i32                dQ turn counter per query tile (turn hand-over)
 //   ctrl   64 i32                           [0] key-block ticket, [32] guard word
 //   part   [nkb, b, h, ntile, kQT * d] f32 dQ partial per key block and query tile (split only)
-//   arrive [b, h] u64                       key blocks finished per (b, h), a byte per XCD (split)
-//   done   [b, h, ntile] u32                1: step 2 summed the tile's dQ (split)
+//   arrive [b, h, nkb] u64                  per key block: the epoch of the launch that finished
+//                                           it, or'ed with its XCD (split)
+//   done   [b, h, ntile] u64                the epoch of the launch whose step 2 summed the tile
+//   epoch  u64 (256 bytes)                  the epoch of the last step 2 launch on the workspace
 // with ntile = ceil(s / kBwdQueryTile), nkb = ceil(s / kBwdKeys). `bytes_min` covers D, turn and
-// ctrl (the turn hand-over), `bytes_split` all six.
+// ctrl (the turn hand-over), `bytes_split` all seven.
 struct Workspace {
-  size_t d_off, turn_off, ctrl_off, part_off, arrive_off, done_off, bytes_min, bytes_split;
+  size_t d_off, turn_off, ctrl_off, part_off, arrive_off, done_off, epoch_off, bytes_min,
+      bytes_split;
 };
 Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d);
 constexpr int kCtrlTicket = 0;
@@ -46,10 +49,16 @@ constexpr int kCtrlGuard = 32;
 // dQ sums inside step 2 (split mode, non-causal, d <= 64): workgroups appended to step 2's grid
 // sum query tiles once every key block of the tile's (b, h) has finished, if all of them ran on
 // the XCD the summing workgroup runs on (their partials then sit in that XCD's L2); step 3 sums
-// the rest. Counts are bytes, so at most kSumMaxBlocks key blocks.
-constexpr int kSumMaxBlocks = 127;
+// the rest. Every step 2 launch carries its own epoch (a 64-bit value unique to the launch, low 3
+// bits zero): the key blocks' arrivals and the done flags hold it, so nothing needs clearing
+// between launches and no stale or uninitialised value passes for a current one (but with a
+// 2^-64 chance). The summing workgroups poll at most kSumMaxBlocks arrival slots.
+constexpr int kSumMaxBlocks = 256;
 // Workgroups appended to step 2's grid for these sums (0: step 3 sums every tile).
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal);
+// Step 3's grid: one workgroup per query tile, or (with step 2's sums) at most 256 workgroups
+// that each check a range of tiles and sum those not done.
+int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal);
 
 // Launchers (fattn_kernels.hip). They assume validated arguments; they return a hipError_t
 // value as int (0 = launched).
@@ -59,18 +68,16 @@ int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl,
                     int s, int d, void* stream);
 // part == nullptr: the turn hand-over (dQ final after step 2; D from step 1); else the split
 // partials, which step 3 (launch_bwd_dq) sums into dQ (D computed from o here, no step 1).
-// arrive / done (split, d <= 64): the counters and flags of step 2's dQ sums, zero at entry.
+// arrive / done / epoch_slot (split, d <= 64): step 2's dQ sums, tagged with `epoch`.
 int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const float* lse,
                     const float* dsum, float* dqkv, float* part, unsigned long long* arrive,
-                    unsigned* done, int* turn, int* ctrl, int b, int h, int s, int d,
+                    unsigned long long* done, unsigned long long* epoch_slot,
+                    unsigned long long epoch, int* turn, int* ctrl, int b, int h, int s, int d,
                     float scale, int causal, void* stream);
-// Step 3: dQ of every query tile whose done flag (done: null, none) is not set.
-int launch_bwd_dq(const float* part, const unsigned* done, float* dqkv, int b, int h, int s,
-                  int d, float scale, int causal, void* stream);
-// Step 1 of the split mode at d <= 64 (step 2 forms D itself): zero the n64 counters at arrive
-// and the n32 flags at done (needed when bwd_sum_blocks is not 0).
-int launch_bwd_clear(unsigned long long* arrive, int64_t n64, unsigned* done, int64_t n32,
-                     void* stream);
+// Step 3: dQ of every query tile that step 2 did not sum (done: null, none did).
+int launch_bwd_dq(const float* part, const unsigned long long* done,
+                  const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
+                  float scale, int causal, void* stream);
 
 // Grid sizes the launchers will use (for range checks before launching).
 int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal, int d);

@@ -32,6 +32,8 @@
 //     dispatch order). Needs no workspace beyond D and the counters.
 #include <hip/hip_runtime.h>
 #include <math.h>
+
+#include <algorithm>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -687,11 +689,14 @@ struct BwdArgs {
   const float* dsum;  // otherwise: D from step 1
   float* dqkv;
   float* part;  // split: the dQ partials, [nkb][b h][ntile][kQT * D] in fragment order
-  // split, D <= 64, null when step 3 sums every tile: key blocks finished per (b, h) (byte x
-  // counts those on XCD x) and the flags of the tiles summed here. Workgroups from n_main on sum
-  // tiles; n_main (the key blocks, rounded up to a multiple of 8) and the sums' layout below.
+  // split, D <= 64, null when step 3 sums every tile: per key block, the epoch of the launch
+  // that finished it or'ed with its XCD; per query tile, the epoch of the launch that summed it
+  // here; the workspace's record of this launch's epoch. Workgroups from n_main on sum tiles;
+  // n_main (the key blocks, rounded up to a multiple of 8) and the sums' layout below.
   unsigned long long* arrive;
-  unsigned* done;
+  unsigned long long* done;
+  unsigned long long* epoch_slot;
+  unsigned long long epoch;
   int n_main;
   int* turn;
   int* ctrl;
@@ -1250,17 +1255,19 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // dispatched. Workgroup n_main + 8 m + x (on XCD x: workgroups go to the XCDs round robin on
 // MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks xcd_remap puts on XCD x:
 // `per` consecutive (b, h)s from x per (the host enables this only when per is whole), kSumTiles
-// tiles per chunk, in the order their key blocks were dispatched. Thread 0 polls the (b, h)'s
-// counter -- an atomic add of 0, at the same coherence point as the key blocks' additions -- until
-// every key block has counted itself (each does so once its partials are stored), sleeping between
-// polls, giving up after kSumPolls. The chunk is summed only if every key block counted itself on
+// tiles per chunk, in the order their key blocks were dispatched. Each key block, once its
+// partials are stored, writes the launch's epoch or'ed with its XCD to its arrival slot (agent
+// scope: written through to the coherence point, as the turn hand-over's counters). Wave 0 polls
+// the (b, h)'s slots (agent-scope loads) until every one holds this launch's epoch, sleeping
+// between polls, giving up after kSumPolls. The chunk is summed only if every key block ran on
 // this workgroup's XCD: all partials are then in this XCD's L2 (or written back from it). The sum
 // is step 3's, operation for operation: float4 i of a tile's partials in key-block order, times
 // scale (so the results are bit-identical whichever kernel sums a tile), stored from fragment
-// order straight into dQ rows (16 lanes write 64 contiguous bytes). Then the chunk's done flags;
-// step 3 sums the tiles without one, so a key block on another XCD, or a poll that gave up, only
-// leaves work to step 3. Every poll ends: the key blocks have smaller workgroup numbers on the same
-// XCD, so they were dispatched before this workgroup and run to completion whatever it does.
+// order straight into dQ rows (16 lanes write 64 contiguous bytes). Then the chunk's done flags
+// (the epoch); step 3 sums the tiles without one, so a key block on another XCD, or a poll that
+// gave up, only leaves work to step 3. Every poll ends: the key blocks have smaller workgroup
+// numbers on the same XCD, so they were dispatched before this workgroup and run to completion
+// whatever it does.
 constexpr int kSumPolls = 4096;
 constexpr int kSumTiles = 3;  // query tiles per summing workgroup (config 2: 1, 2, 15 slower; 4 same)
 template <int D>
@@ -1272,18 +1279,27 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
   if (m >= per * nchunk) return;
   const int bh = x * per + m / nchunk;
   const int j0 = (m % nchunk) * kSumTiles, j1 = min(ntile, j0 + kSumTiles);
-  unsigned xcc;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-  const unsigned long long mine = static_cast<unsigned long long>(nkb) << (8 * (xcc & 7u));
-  if (tid == 0) {
-    unsigned long long v = 0;
+  if (tid < 64) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const unsigned long long mine = a.epoch | (xcc & 7u);
+    const unsigned long long* slots = a.arrive + static_cast<int64_t>(bh) * nkb;
+    bool all_mine = false;
     for (int it = 0; it < kSumPolls; ++it) {
-      v = __hip_atomic_fetch_add(a.arrive + bh, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // Sum of the bytes (each below 128): key blocks finished on any XCD.
-      if (static_cast<int>((v * 0x0101010101010101ull) >> 56) >= nkb) break;
+      bool arrived = true, here = true;
+      for (int kb = tid; kb < nkb; kb += 64) {
+        const unsigned long long v =
+            __hip_atomic_load(slots + kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        arrived = arrived && (v & ~7ull) == a.epoch;
+        here = here && v == mine;
+      }
+      if (__builtin_amdgcn_ballot_w64(!arrived) == 0) {
+        all_mine = __builtin_amdgcn_ballot_w64(!here) == 0;
+        break;
+      }
       __builtin_amdgcn_s_sleep(16);  // about 1000 cycles between polls
     }
-    *flag = v == mine ? 1u : 0u;
+    if (tid == 0) *flag = all_mine ? 1u : 0u;
   }
   __syncthreads();
   if (*flag == 0u) return;
@@ -1319,7 +1335,7 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
       }
     }
   }
-  if (tid < j1 - j0) a.done[static_cast<int64_t>(bh) * ntile + j0 + tid] = 1u;
+  if (tid < j1 - j0) a.done[static_cast<int64_t>(bh) * ntile + j0 + tid] = a.epoch;
 }
 
 template <int D>
@@ -1351,6 +1367,7 @@ bwd_split_kernel(BwdArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
   const int BH = a.B * a.H, S = a.S;
   const int id = static_cast<int>(blockIdx.x);
+  if (a.arrive != nullptr && id == 0 && tid == 0) *a.epoch_slot = a.epoch;  // for step 3
   if (a.arrive != nullptr && id >= a.nkb * BH) {
     // A dQ sum (the grid's last workgroups; those below n_main pad it to a multiple of 8).
     if (id >= a.n_main) bwd_sum_tiles<D>(a, id & 7, (id - a.n_main) >> 3, &sm.flag);
@@ -1568,15 +1585,15 @@ bwd_split_kernel(BwdArgs a) {
   if (wave_dq) store_frag(t0 + nsteps - 1);  // the last tile's fragment
   if (a.arrive != nullptr) {
     // Every partial of this key block is stored once the stores of every wave have completed:
-    // count the block, in the byte of the XCD it runs on (dK and dV, stored below, are not read
-    // by the sums).
+    // record its arrival, with the XCD it runs on (dK and dV, stored below, are not read by the
+    // sums).
     wait_mem();
     __syncthreads();
     if (tid == 0) {
       unsigned xcc;
       asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-      __hip_atomic_fetch_add(a.arrive + bh, 1ull << (8 * (xcc & 7u)), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.arrive + static_cast<int64_t>(bh) * a.nkb + kb, a.epoch | (xcc & 7u),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
@@ -1594,32 +1611,20 @@ bwd_split_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Backward, step 3 (split only): dQ of one (b, h, query tile) per workgroup, the tile's partials
-// summed in key-block order, ((p_0 + p_1) + p_2) + ..., times scale (the same operations, in the
-// same order, as the turn hand-over). Float4 i of a partial (fragment order: dim tile dt = i / 64
-// of subtile m, lane l = i % 64, registers r = 0..3 -> query 16 m + 4 (l / 16) + r, dim
-// 16 dt + l % 16) is summed by one thread, then the tile goes through LDS so that every row of dQ
-// is written as D / 4 float4s.
+// Backward, step 3 (split only): dQ of a (b, h, query tile), the tile's partials summed in
+// key-block order, ((p_0 + p_1) + p_2) + ..., times scale (the same operations, in the same order,
+// as the turn hand-over and as step 2's own sums). Float4 i of a partial (fragment order: dim tile
+// dt = i / 64 of subtile m, lane l = i % 64, registers r = 0..3 -> query 16 m + 4 (l / 16) + r,
+// dim 16 dt + l % 16) is summed by one thread, then the tile goes through LDS so that every row of
+// dQ is written as D / 4 float4s.
 // ---------------------------------------------------------------------------------------------
 template <int D>
-__global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ part,
-                                                     const unsigned* __restrict__ done,
-                                                     float* __restrict__ dqkv, int B, int H,
-                                                     int S, int nkb, int ntile, float scale,
-                                                     int causal) {
+__device__ __forceinline__ void dq_tile(const float* __restrict__ part, float* __restrict__ dqkv,
+                                        int B, int H, int S, int nkb, int ntile, float scale,
+                                        int causal, int bh, int j, float* tile) {
   constexpr int kDT = D / 16, kPitch = D + 4;  // pitch: conflict-free fragment writes
   constexpr int kF4 = kQT * D / 4;             // float4s per tile
-  __shared__ __attribute__((aligned(16))) float tile[kQT * kPitch];
   const int tid = threadIdx.x;
-  // Non-causal: the tiles of a (b, h) on the XCD that ran its key blocks in step 2 (the same
-  // XCD-major split of the grid), the (b, h) written last first, whose partials are likeliest
-  // still cached.
-  const int tot = B * H * ntile;
-  int it = static_cast<int>(blockIdx.x);
-  if (!causal && it < (tot & ~7)) it = (it & 7) * (tot >> 3) + ((tot >> 3) - 1 - (it >> 3));
-  const int bh = it / ntile, j = it % ntile;
-  // Tiles step 2 summed are done.
-  if (done != nullptr && done[static_cast<int64_t>(bh) * ntile + j] != 0u) return;
   const int b = bh / H, h = bh % H, q0 = j * kQT;
   // Contributors: causal, the key blocks holding a key <= the tile's last query.
   const int cnt = causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) + 1 : nkb;
@@ -1657,14 +1662,42 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
   }
 }
 
-// Backward, step 1 of the split mode at D <= 64 (step 2 forms D itself): zero the counters and
-// done flags of step 2's dQ sums.
-__global__ void __launch_bounds__(kThreads) clear_kernel(unsigned long long* __restrict__ arrive,
-                                                         int64_t n64, unsigned* __restrict__ done,
-                                                         int64_t n32) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (i < n64) arrive[i] = 0ull;
-  if (i < n32) done[i] = 0u;
+// One workgroup per query tile (done == null), or, after step 2's own sums, each workgroup checks
+// a range of up to kThreads tiles (one flag per thread) and sums those whose flag does not hold
+// the epoch of the step 2 launch (recorded in the workspace), one after the other.
+template <int D>
+__global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ part,
+                                                     const unsigned long long* __restrict__ done,
+                                                     const unsigned long long* __restrict__ epoch,
+                                                     float* __restrict__ dqkv, int B, int H,
+                                                     int S, int nkb, int ntile, float scale,
+                                                     int causal) {
+  __shared__ __attribute__((aligned(16))) float tile[kQT * (D + 4)];
+  __shared__ int todo[kThreads];
+  __shared__ int ntodo;
+  const int tot = B * H * ntile;
+  if (done == nullptr) {
+    // Non-causal: the tiles of a (b, h) on the XCD that ran its key blocks in step 2 (the same
+    // XCD-major split of the grid), the (b, h) written last first, whose partials are likeliest
+    // still cached.
+    int it = static_cast<int>(blockIdx.x);
+    if (!causal && it < (tot & ~7)) it = (it & 7) * (tot >> 3) + ((tot >> 3) - 1 - (it >> 3));
+    dq_tile<D>(part, dqkv, B, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile, tile);
+    return;
+  }
+  const int tid = threadIdx.x;
+  const int per = (tot + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+  const int first = static_cast<int>(blockIdx.x) * per, n = min(per, tot - first);
+  if (tid == 0) ntodo = 0;
+  __syncthreads();
+  if (tid < n && done[first + tid] != *epoch) todo[atomicAdd(&ntodo, 1)] = first + tid;
+  __syncthreads();
+  const int k = ntodo;
+  for (int i = 0; i < k; ++i) {
+    const int it = todo[i];
+    dq_tile<D>(part, dqkv, B, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile, tile);
+    __syncthreads();  // the LDS tile is reused
+  }
 }
 
 }  // namespace
@@ -1747,14 +1780,13 @@ int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
   const int64_t f = ((nkb * bh) & ~int64_t{7}) / 8;
   return f % nkb == 0 && f > 0 ? 8 * (f / nkb) * nchunk : 0;
 }
-
-int launch_bwd_clear(unsigned long long* arrive, int64_t n64, unsigned* done, int64_t n32,
-                     void* stream) {
-  void* args[] = {&arrive, &n64, &done, &n32};
-  const int64_t n = n64 > n32 ? n64 : n32;
-  return static_cast<int>(launch(reinterpret_cast<const void*>(clear_kernel),
-                                 (n + kThreads - 1) / kThreads, args, stream));
+int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  const int64_t tiles = bwd_dq_blocks(b, h, s);
+  if (bwd_sum_blocks(b, h, s, d, causal) == 0) return tiles;
+  const int64_t g = std::max<int64_t>(256, (tiles + kThreads - 1) / kThreads);
+  return std::min(tiles, g);
 }
+
 
 int launch_forward(View q, View k, View v, float* o, float* lse, int b, int h, int s, int d,
                    float scale, int causal, void* stream) {
@@ -1780,16 +1812,17 @@ int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl,
 
 int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const float* lse,
                     const float* dsum, float* dqkv, float* part, unsigned long long* arrive,
-                    unsigned* done, int* turn, int* ctrl, int b, int h, int s, int d,
+                    unsigned long long* done, unsigned long long* epoch_slot,
+                    unsigned long long epoch, int* turn, int* ctrl, int b, int h, int s, int d,
                     float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
   const bool split = part != nullptr;
   const int stagger = !split && !causal && nkb <= kStaggerMaxBlocks ? 1 : 0;
   const int64_t nsum = split ? bwd_sum_blocks(b, h, s, d, causal) : 0;
   const int64_t nmain = (bwd_main_blocks(b, h, s) + 7) & ~int64_t{7};
-  if (nsum == 0) arrive = nullptr, done = nullptr;
-  BwdArgs a{q, k, v, d_o, o, lse, dsum, dqkv, part, arrive, done, static_cast<int>(nmain),
-            turn, ctrl, b, h, s, nkb, ntile, scale, causal, stagger};
+  if (nsum == 0) arrive = nullptr, done = nullptr, epoch_slot = nullptr;
+  BwdArgs a{q,    k,     v,    d_o,  o, lse, dsum, dqkv, part, arrive, done, epoch_slot, epoch,
+            static_cast<int>(nmain), turn, ctrl, b, h, s, nkb, ntile, scale, causal, stagger};
   void* args[] = {&a};
   if (split && d <= 64) {
     const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32>)
@@ -1810,15 +1843,16 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
 }
 
-int launch_bwd_dq(const float* part, const unsigned* done, float* dqkv, int b, int h, int s,
-                  int d, float scale, int causal, void* stream) {
+int launch_bwd_dq(const float* part, const unsigned long long* done,
+                  const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
+                  float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
-  if (bwd_sum_blocks(b, h, s, d, causal) == 0) done = nullptr;
-  void* args[] = {&part, &done, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
+  if (bwd_sum_blocks(b, h, s, d, causal) == 0) done = nullptr, epoch_slot = nullptr;
+  void* args[] = {&part, &done, &epoch_slot, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
   const void* fn = d == 32    ? reinterpret_cast<const void*>(dq_kernel<32>)
                    : d == 128 ? reinterpret_cast<const void*>(dq_kernel<128>)
                               : reinterpret_cast<const void*>(dq_kernel<64>);
-  return static_cast<int>(launch(fn, bwd_dq_blocks(b, h, s), args, stream));
+  return static_cast<int>(launch(fn, bwd_dq_grid(b, h, s, d, causal), args, stream));
 }
 
 }  // namespace fattn
