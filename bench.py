@@ -159,8 +159,8 @@ def main() -> int:
     # Per-kernel durations: K more steps, back to back as above, with the backward launched as
     # its kernel-level steps (the same kernels on the same arguments as fattn_qkv_backward) and a
     # HIP event on the launch stream between every two launches.
-    # With a split workspace at d 64, step 1 only clears the counters of the dQ sums that step 2's
-    # last workgroups do (step 2 computes D itself); step 3 sums the tiles those left.
+    # With a split workspace at d 64 step 1 launches nothing (step 2 computes D itself, and its
+    # last workgroups sum dQ tiles); step 3 sums the tiles those left.
     kernels = [("fwd", fwd), ("bwd_prep", prep_k), ("bwd_main", main_k)]
     if split:
         kernels.append(("bwd_dq", dq_k))

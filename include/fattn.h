@@ -84,10 +84,9 @@ size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s, int64_t 
 
 /* Backward step 1: D[b, h, i] = sum_c dO[b, i, h, c] * O[b, i, h, c] (fixed order) and the
  * counters of step 2 cleared. O is [b, s, h, d] contiguous; dO is read through do_strides. With
- * a split-size workspace at d <= 64 step 2 computes D itself, and this step only clears the
- * counters of the dQ sums step 2's last workgroups do. It must run before step 2 on the same
- * workspace, in every mode. Replaces the fattn_bwd_dot_f32_d64 launch (src/cuda.rs:215-231),
- * which also clears counters. */
+ * a split-size workspace at d <= 64 there is nothing to do (step 2 computes D itself, and tags
+ * the state of its own dQ sums with a value unique to its launch; returns 0 after the checks).
+ * Replaces the fattn_bwd_dot_f32_d64 launch (src/cuda.rs:215-231). */
 int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_strides[3],
                        void* workspace, size_t workspace_bytes, int64_t b, int64_t h, int64_t s,
                        int64_t d, void* stream);
@@ -96,9 +95,9 @@ int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_stride
  * gradient layout); dQ summed over key blocks in a fixed order, so every rerun is bit-identical:
  * with a split-size workspace its partials go to the workspace (this step sums some query
  * tiles, step 3 the rest) and, for d <= 64, D is computed here from O (the forward's
- * [b, s, h, d] output); else dQ is complete after this step. Step 1 must run first on the same
- * workspace (it clears the counters, or computes D). Replaces the fattn_bwd_f32_d64 launch
- * (src/cuda.rs:233-258), which takes no O. */
+ * [b, s, h, d] output); else dQ is complete after this step. Where D is not computed here it
+ * comes from step 1, which must run first on the same workspace (running step 1 first is always
+ * correct). Replaces the fattn_bwd_f32_d64 launch (src/cuda.rs:233-258), which takes no O. */
 int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const float* o,
                        const float* d_o, const float* lse, float* dqkv, void* workspace,
                        size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
@@ -107,11 +106,12 @@ int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const flo
                        const int64_t do_strides[3], void* stream);
 
 /* Backward step 3: with a split-size workspace, dQ = scale * (sum of step 2's partials in
- * key-block order) into part 0 of dqkv, for every query tile step 2 did not sum itself (its last
- * workgroups sum the tiles of (b, h)s whose key blocks all ran on their XCD; non-causal, d <= 64;
- * the same operations in the same order, so the result does not depend on which kernel summed a
- * tile); with a smaller workspace nothing to do (returns 0). Has no counterpart launch in the
- * reference (its dQ is summed in place, as the turn mode here). */
+ * key-block order) into part 0 of dqkv, for every query tile the last step 2 launch on this
+ * workspace did not sum itself (its last workgroups sum the tiles of (b, h)s whose key blocks all
+ * ran on their XCD; non-causal, d <= 64; the same operations in the same order, so the result
+ * does not depend on which kernel summed a tile); with a smaller workspace nothing to do (returns
+ * 0). Has no counterpart launch in the reference (its dQ is summed in place, as the turn mode
+ * here). */
 int fattn_bwd_dq_f32(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                      int64_t s, int64_t d, float scale, int causal, void* stream);
 
