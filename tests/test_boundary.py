@@ -53,12 +53,12 @@ def test_workspace_size_is_aligned_and_monotone():
     # minimum: D (64*6*240 f32) + turns (64*6*15 i32) + control
     assert lo >= 64 * 6 * 240 * 4 + 64 * 6 * 15 * 4 + 256
     # split: plus one 16 x d f32 partial per key block (4) and query tile (15) of each (b, h), a
-    # u64 arrival counter per (b, h) and a u32 done flag per query tile (both 256-byte multiples
-    # here)
+    # u64 arrival slot per key block and a u64 done flag per query tile (both 256-byte multiples
+    # here) and 256 bytes for the epoch of the last step 2 launch
     for d in (32, 64, 128):
         assert L.fattn_bwd_workspace_min_bytes(64, 6, 240, d) == lo
         assert (L.fattn_bwd_workspace_split_bytes(64, 6, 240, d)
-                == lo + 4 * 64 * 6 * 15 * 16 * d * 4 + 64 * 6 * 8 + 64 * 6 * 15 * 4)
+                == lo + 4 * 64 * 6 * 15 * 16 * d * 4 + 64 * 6 * 4 * 8 + 64 * 6 * 15 * 8 + 256)
     assert n1 == hi  # 94 MB: below the split cap
     assert L.fattn_bwd_workspace_bytes(64, 6, 241, 64) >= n1
     assert L.fattn_bwd_workspace_bytes(-1, 6, 240, 64) == 0
