@@ -46,8 +46,8 @@ struct Workspace {
 Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d);
 constexpr int kCtrlTicket = 0;
 constexpr int kCtrlGuard = 32;
-// dQ sums inside step 2 (split mode, non-causal, d <= 64): workgroups appended to step 2's grid
-// sum query tiles once every key block of the tile's (b, h) has finished, if all of them ran on
+// dQ sums inside step 2 (split mode, d <= 64): workgroups appended to step 2's grid sum query
+// tiles once every key block the tiles need has finished, if all of them ran on
 // the XCD the summing workgroup runs on (their partials are then in that XCD's L2 or written back
 // from it, so it reads them coherently); step 3 sums the rest. Every step 2 launch carries its own epoch (a 64-bit value unique to the launch, low 3
 // bits zero): the key blocks' arrivals and the done flags hold it, so nothing needs clearing

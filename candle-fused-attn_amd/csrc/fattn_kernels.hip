@@ -1249,13 +1249,14 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // folds such offsets into the LDS instructions, where across separate arrays it keeps an address
 // register per array (at D 64 that saves 24 registers).
 // ---------------------------------------------------------------------------------------------
-// dQ sums inside step 2 (split, non-causal, D <= 64). Step 3 moves 118 MB at config 2 after step
+// dQ sums inside step 2 (split, D <= 64). Step 3 moves 118 MB at config 2 after step
 // 2's tail, where the CUs run fewer and fewer key blocks; workgroups appended to step 2's grid do
 // its sums in that tail instead. In-order dispatch starts them only once every key block has been
 // dispatched. Workgroup n_main + 8 m + x (on XCD x: workgroups go to the XCDs round robin on
 // MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks xcd_remap puts on XCD x:
 // `per` consecutive (b, h)s from x per (the host enables this only when per is whole), kSumTiles
-// tiles per chunk, in the order their key blocks were dispatched. Each key block, once its
+// tiles per chunk, in the order their key blocks were dispatched (causal: see the mapping below;
+// a chunk then waits only for the key blocks its tiles need). Each key block, once its
 // partials are stored, writes the launch's epoch or'ed with its XCD to its arrival slot (agent
 // scope: written through to the coherence point, as the turn hand-over's counters). Wave 0 polls
 // the (b, h)'s slots (agent-scope loads) until every one holds this launch's epoch, sleeping
@@ -1275,10 +1276,18 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
   constexpr int kDT = D / 16, kF4 = kQT * D / 4;
   const int tid = threadIdx.x, BH = a.B * a.H, ntile = a.ntile, nkb = a.nkb;
   const int nchunk = (ntile + kSumTiles - 1) / kSumTiles;
-  const int per = ((a.n_main & ~7) >> 3) / nkb;
+  // Non-causal: the (b, h)s whose key blocks xcd_remap put on XCD x, one (b, h) after the other.
+  // Causal: key block kb of (b, h) is workgroup kb b h + bh, on XCD bh mod 8 when 8 divides b h;
+  // the chunks go tile-major (a tile's contributors are the key blocks up to its last query, so
+  // the first tiles are complete first).
+  const int per = a.causal ? BH / 8 : ((a.n_main & ~7) >> 3) / nkb;
   if (m >= per * nchunk) return;
-  const int bh = x * per + m / nchunk;
-  const int j0 = (m % nchunk) * kSumTiles, j1 = min(ntile, j0 + kSumTiles);
+  const int bh = a.causal ? x + 8 * (m % per) : x * per + m / nchunk;
+  const int j0 = (a.causal ? m / per : m % nchunk) * kSumTiles;
+  const int j1 = min(ntile, j0 + kSumTiles);
+  // Key blocks whose partials the chunk needs: all, or (causal) those holding a key <= its last
+  // query.
+  const int need = a.causal ? min(nkb - 1, min(a.S - 1, j1 * kQT - 1) / kBwdKeys) + 1 : nkb;
   if (tid < 64) {
     unsigned xcc;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
@@ -1287,7 +1296,7 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
     bool all_mine = false;
     for (int it = 0; it < kSumPolls; ++it) {
       bool arrived = true, here = true;
-      for (int kb = tid; kb < nkb; kb += 64) {
+      for (int kb = tid; kb < need; kb += 64) {
         const unsigned long long v =
             __hip_atomic_load(slots + kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         arrived = arrived && (v & ~7ull) == a.epoch;
@@ -1310,12 +1319,13 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
       a.dqkv + static_cast<int64_t>(b) * S * row_stride + static_cast<int64_t>(h) * D;
   for (int j = j0; j < j1; ++j) {
     const int q0 = j * kQT;
+    const int cnt = a.causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) + 1 : nkb;
     const float* src = a.part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D);
 #pragma unroll
     for (int i = tid; i < kF4; i += kThreads) {
       f4 acc = ld4(src + 4 * i);
       int kb = 1;
-      for (; kb + 3 < nkb; kb += 4) {
+      for (; kb + 3 < cnt; kb += 4) {
         const f4 x0 = ld4(src + kb * slot + 4 * i), x1 = ld4(src + (kb + 1) * slot + 4 * i);
         const f4 x2 = ld4(src + (kb + 2) * slot + 4 * i), x3 = ld4(src + (kb + 3) * slot + 4 * i);
         acc += x0;
@@ -1323,7 +1333,7 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
         acc += x2;
         acc += x3;
       }
-      for (; kb < nkb; ++kb) acc += ld4(src + kb * slot + 4 * i);
+      for (; kb < cnt; ++kb) acc += ld4(src + kb * slot + 4 * i);
       acc *= a.scale;
       // Fragment order: register r of float4 i is query q0 + 16 mm + 4 g + r, dim 16 dt + lo.
       const int lane = i & 63, md = i >> 6, dt = md % kDT, mm = md / kDT;
@@ -1772,10 +1782,10 @@ int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQ
 bool bwd_needs_prep(bool split, int d) { return !split || d > 64; }
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
   const int64_t nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT, bh = b * h;
-  // Causal: every (b, h) finishes near the end of step 2 (its key blocks are spread over the whole
-  // key-block-major order), so its sums would only lengthen the kernel (config 3: +4 %).
-  if (causal || d > 64 || nkb > kSumMaxBlocks) return 0;
+  if (d > 64 || nkb > kSumMaxBlocks) return 0;
   const int64_t nchunk = (ntile + kSumTiles - 1) / kSumTiles;
+  // Causal: the key blocks of a (b, h) share an XCD when 8 divides b h.
+  if (causal) return bh % 8 == 0 ? bh * nchunk : 0;
   // Non-causal: XCD x holds key blocks [x F, (x + 1) F) of the (b h)-major order, F = full / 8.
   const int64_t f = ((nkb * bh) & ~int64_t{7}) / 8;
   return f % nkb == 0 && f > 0 ? 8 * (f / nkb) * nchunk : 0;

@@ -107,8 +107,8 @@ int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const flo
 
 /* Backward step 3: with a split-size workspace, dQ = scale * (sum of step 2's partials in
  * key-block order) into part 0 of dqkv, for every query tile the last step 2 launch on this
- * workspace did not sum itself (its last workgroups sum the tiles of (b, h)s whose key blocks all
- * ran on their XCD; non-causal, d <= 64; the same operations in the same order, so the result
+ * workspace did not sum itself (its last workgroups sum the tiles whose contributing key blocks
+ * all ran on their XCD; d <= 64; the same operations in the same order, so the result
  * does not depend on which kernel summed a tile); with a smaller workspace nothing to do (returns
  * 0). Has no counterpart launch in the reference (its dQ is summed in place, as the turn mode
  * here). */
