@@ -248,9 +248,10 @@ int run_bwd_dq(const char* who, float* dqkv, void* ws, size_t ws_bytes, int64_t 
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
   if (!p.part) return ok();
-  const int err = fattn::launch_bwd_dq(p.part, p.done, p.epoch, dqkv, static_cast<int>(b),
-                                       static_cast<int>(h), static_cast<int>(s),
-                                       static_cast<int>(d), scale, causal ? 1 : 0, stream);
+  const int err = fattn::launch_bwd_dq(p.part, p.done, p.arrive, p.epoch, dqkv,
+                                       static_cast<int>(b), static_cast<int>(h),
+                                       static_cast<int>(s), static_cast<int>(d), scale,
+                                       causal ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 3 launch");
   return ok();
 }

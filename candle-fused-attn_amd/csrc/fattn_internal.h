@@ -74,8 +74,9 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
                     unsigned long long* done, unsigned long long* epoch_slot,
                     unsigned long long epoch, int* turn, int* ctrl, int b, int h, int s, int d,
                     float scale, int causal, void* stream);
-// Step 3: dQ of every query tile that step 2 did not sum (done: null, none did).
-int launch_bwd_dq(const float* part, const unsigned long long* done,
+// Step 3: dQ of every query tile that step 2 did not sum (done: null, none did); then the done
+// flags and arrival slots are zeroed.
+int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long long* arrive,
                   const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
                   float scale, int causal, void* stream);
 

@@ -1674,10 +1674,14 @@ __device__ __forceinline__ void dq_tile(const float* __restrict__ part, float* _
 
 // One workgroup per query tile (done == null), or, after step 2's own sums, each workgroup checks
 // a range of up to kThreads tiles (one flag per thread) and sums those whose flag does not hold
-// the epoch of the step 2 launch (recorded in the workspace), one after the other.
+// the epoch of the step 2 launch (recorded in the workspace), one after the other. It then zeroes
+// the flags it read and a range of the key blocks' arrival slots: every backward leaves that state
+// clear, so a launch whose epoch repeats (a replayed graph bakes in its launch arguments) never
+// meets its own earlier values.
 template <int D>
 __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ part,
-                                                     const unsigned long long* __restrict__ done,
+                                                     unsigned long long* __restrict__ done,
+                                                     unsigned long long* __restrict__ arrive,
                                                      const unsigned long long* __restrict__ epoch,
                                                      float* __restrict__ dqkv, int B, int H,
                                                      int S, int nkb, int ntile, float scale,
@@ -1700,7 +1704,14 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
   const int first = static_cast<int>(blockIdx.x) * per, n = min(per, tot - first);
   if (tid == 0) ntodo = 0;
   __syncthreads();
-  if (tid < n && done[first + tid] != *epoch) todo[atomicAdd(&ntodo, 1)] = first + tid;
+  if (tid < n) {
+    if (done[first + tid] != *epoch) todo[atomicAdd(&ntodo, 1)] = first + tid;
+    done[first + tid] = 0ull;
+  }
+  const int nslot = B * H * nkb;
+  const int per_slot = (nslot + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+  const int slot0 = static_cast<int>(blockIdx.x) * per_slot;
+  if (tid < min(per_slot, nslot - slot0)) arrive[slot0 + tid] = 0ull;
   __syncthreads();
   const int k = ntodo;
   for (int i = 0; i < k; ++i) {
@@ -1853,12 +1864,15 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
 }
 
-int launch_bwd_dq(const float* part, const unsigned long long* done,
+int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long long* arrive,
                   const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
                   float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
-  if (bwd_sum_blocks(b, h, s, d, causal) == 0) done = nullptr, epoch_slot = nullptr;
-  void* args[] = {&part, &done, &epoch_slot, &dqkv, &b, &h, &s, &nkb, &ntile, &scale, &causal};
+  if (bwd_sum_blocks(b, h, s, d, causal) == 0) {
+    done = nullptr, arrive = nullptr, epoch_slot = nullptr;
+  }
+  void* args[] = {&part,  &done, &arrive, &epoch_slot, &dqkv,  &b,
+                  &h,     &s,    &nkb,    &ntile,      &scale, &causal};
   const void* fn = d == 32    ? reinterpret_cast<const void*>(dq_kernel<32>)
                    : d == 128 ? reinterpret_cast<const void*>(dq_kernel<128>)
                               : reinterpret_cast<const void*>(dq_kernel<64>);

@@ -516,6 +516,67 @@ def test_dq_sums_in_step2_match_step3(orc, cuda, h, s):
                  ref_grad, "head 0")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_graph_replays(orc, cuda, causal):
+    """Forward and backward (qkv entries of the C ABI) captured in one HIP graph and replayed on
+    new inputs each time: every replay equals an eager run on the same inputs bit for bit. A replay
+    repeats its launch arguments, step 2's dQ-sum epoch included, so this holds only because each
+    backward leaves the sums' state clear (with stale state, a replay's sums would take the
+    previous replay's partials). Eager work (new inputs, an eager run on the same workspace) and
+    synchronisations run between the replays."""
+    b, h, s, d = 8, 6, 240, 64  # 8 divides b h: step 2 sums dQ tiles, causal too
+    L = _lib.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    qkv = torch.empty(b, s, 3 * h * d, device=cuda)
+    dout = torch.empty(b, s, h * d, device=cuda)
+    out = torch.empty(b, s, h * d, device=cuda)
+    lse = torch.empty(b, h, s, device=cuda)
+    dqkv = torch.empty_like(qkv)
+    nbytes = L.fattn_bwd_workspace_bytes(b, h, s, d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=cuda)
+    shape, strides = _lib.arr(qkv.shape), _lib.arr(qkv.stride())
+    gshape, gstrides = _lib.arr(dout.shape), _lib.arr(dout.stride())
+    ci = 1 if causal else 0
+
+    def step():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(L.fattn_qkv_forward(P(qkv), 0, shape, strides, h, 0.125, ci, P(out), P(lse),
+                                       st))
+        _lib.check(L.fattn_qkv_backward(P(qkv), 0, shape, strides, h, 0.125, ci, P(out), P(lse),
+                                        P(dout), 0, gshape, gstrides, P(dqkv), P(ws), nbytes, st))
+
+    gen = torch.Generator().manual_seed(7)
+    qkv.copy_(torch.randn(qkv.shape, generator=gen))
+    dout.copy_(torch.randn(dout.shape, generator=gen))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # warm-up on a side stream before capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for r in range(4):
+        say(f"graph replay {r} causal={causal}")
+        qkv.copy_(torch.randn(qkv.shape, generator=gen))
+        dout.copy_(torch.randn(dout.shape, generator=gen))
+        dqkv.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got_o, got_g = bits(out).clone(), bits(dqkv).clone()
+        dqkv.zero_()
+        step()  # eager, same inputs, same workspace
+        torch.cuda.synchronize()
+        assert torch.equal(got_o, bits(out)), f"replay {r}: O"
+        assert torch.equal(got_g, bits(dqkv)), f"replay {r}: gradient"
+    # the last replay against the fp64 oracle
+    x, w = qkv.cpu().numpy(), dout.cpu().numpy()
+    ref_out, _, ref_grad = oracle_qkv(orc, x, w, h, d, causal, np.float64, 0.125)
+    check_errors(orc, out, dqkv, ref_out, ref_grad, "after replays")
+
+
 # --- head_dim 32 and 128 (the reference's roadmap, ROADMAP.md:76-79) ------------------------
 
 @pytest.mark.parametrize("d", [32, 128])
