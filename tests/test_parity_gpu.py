@@ -490,30 +490,56 @@ def test_split_and_turns_agree(orc, cuda, causal):
             assert rel <= 1e-6
 
 
-@pytest.mark.parametrize("h,s", [(9, 240), (9, 100), (17, 50)])
-def test_dq_sums_in_step2_match_step3(orc, cuda, h, s):
+@pytest.mark.parametrize("d,h,s", [(64, 9, 240), (64, 9, 100), (64, 17, 50), (32, 9, 240),
+                                   (32, 17, 100)])
+def test_dq_sums_in_step2_match_step3(orc, cuda, d, h, s):
     """Non-causal split backward: the last workgroups of step 2 sum the dQ tiles of the (b, h)s
-    whose key blocks an XCD ran (with workgroups dealt to the XCDs round robin, here heads
-    0-7, or 0-15 at s 50), step 3 the rest (head 8, or 16): the same operations in the same order.
-    With every head given the same q, k, v and output gradient, every head's O, dQ, dK and dV must
-    be bit-identical, whichever kernel summed it; head 0 is checked against the fp64 oracle."""
-    rng = np.random.default_rng(11)
-    one = rng.standard_normal((1, s, 3, 1, 64)).astype(np.float32)
-    x = np.ascontiguousarray(np.broadcast_to(one, (1, s, 3, h, 64))).reshape(1, s, 3 * h * 64)
-    w1 = rng.standard_normal((1, s, 1, 64)).astype(np.float32)
-    w = np.ascontiguousarray(np.broadcast_to(w1, (1, s, h, 64))).reshape(1, s, h * 64)
-    say(f"dq sums b1 h{h} s{s}")
-    out, grad = run("fused_qkv", torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), h, 64,
+    whose key blocks an XCD ran (with workgroups dealt to the XCDs round robin: heads 0-7, or 0-15
+    where 2 h key blocks or fewer), step 3 the rest (the last head): the same operations in the
+    same order. With every head given the same q, k, v and output gradient, every head's O, dQ, dK
+    and dV must be bit-identical, whichever kernel summed it; head 0 is checked against the fp64
+    oracle."""
+    rng = np.random.default_rng(11 + d)
+    one = rng.standard_normal((1, s, 3, 1, d)).astype(np.float32)
+    x = np.ascontiguousarray(np.broadcast_to(one, (1, s, 3, h, d))).reshape(1, s, 3 * h * d)
+    w1 = rng.standard_normal((1, s, 1, d)).astype(np.float32)
+    w = np.ascontiguousarray(np.broadcast_to(w1, (1, s, h, d))).reshape(1, s, h * d)
+    say(f"dq sums d{d} b1 h{h} s{s}")
+    out, grad = run("fused_qkv", torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), h, d,
                     False, 0.125)
-    o = out.reshape(1, s, h, 64)
-    g = grad.reshape(1, s, 3, h, 64)
+    o = out.reshape(1, s, h, d)
+    g = grad.reshape(1, s, 3, h, d)
     for i in range(1, h):
         assert torch.equal(bits(o[:, :, i]), bits(o[:, :, 0])), f"O of head {i}"
         assert torch.equal(bits(g[:, :, :, i]), bits(g[:, :, :, 0])), f"gradient of head {i}"
-    ref_out, _, ref_grad = oracle_qkv(orc, one.reshape(1, s, 3 * 64), w1.reshape(1, s, 64), 1, 64,
+    ref_out, _, ref_grad = oracle_qkv(orc, one.reshape(1, s, 3 * d), w1.reshape(1, s, d), 1, d,
                                       False, np.float64, 0.125)
-    check_errors(orc, o[:, :, 0].contiguous(), g[:, :, :, 0].reshape(1, s, 3 * 64), ref_out,
+    check_errors(orc, o[:, :, 0].contiguous(), g[:, :, :, 0].reshape(1, s, 3 * d), ref_out,
                  ref_grad, "head 0")
+
+
+@pytest.mark.parametrize("d", [32, 64])
+def test_causal_dq_sums_match_turns(orc, cuda, d):
+    """Causal split backward with 8 | b h (step 2's last workgroups sum the dQ tiles, each waiting
+    only for the key blocks its tiles need) against the turn hand-over, which sums dQ in place in
+    the same key-block order: O and the whole gradient bit-identical, and within the fp64 bar."""
+    b, h, s = 2, 4, 200
+    rng = np.random.default_rng(5 + d)
+    x = rng.standard_normal((b, s, 3 * h * d)).astype(np.float32)
+    w = rng.standard_normal((b, s, h * d)).astype(np.float32)
+    qkv, wt = torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda)
+    res = {}
+    for mode in ("split", "turns"):
+        say(f"causal sums d{d} {mode}")
+        prev = cfa.set_dq_sum(mode)
+        try:
+            res[mode] = run("fused_qkv", qkv, wt, h, d, True, 0.125)
+        finally:
+            cfa.set_dq_sum(prev)
+    (o1, g1), (o2, g2) = res["split"], res["turns"]
+    assert torch.equal(bits(o1), bits(o2)) and torch.equal(bits(g1), bits(g2))
+    ref_out, _, ref_grad = oracle_qkv(orc, x, w, h, d, True, np.float64, 0.125)
+    check_errors(orc, o1, g1, ref_out, ref_grad, f"causal d{d}")
 
 
 @pytest.mark.parametrize("causal", [False, True])
