@@ -1317,31 +1317,52 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
   const int64_t row_stride = static_cast<int64_t>(3) * a.H * D;
   float* const dq_bh =
       a.dqkv + static_cast<int64_t>(b) * S * row_stride + static_cast<int64_t>(h) * D;
-  for (int j = j0; j < j1; ++j) {
-    const int q0 = j * kQT;
-    const int cnt = a.causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) + 1 : nkb;
-    const float* src = a.part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D);
+  // Thread i sums float4 i of each of the chunk's tiles, four key blocks at a time: the loads of
+  // all the chunk's tiles for those key blocks are issued together, then added in key-block order.
+  static_assert(kF4 <= kThreads, "one float4 of each tile per thread");
+  const int i = tid;
+  if (i < kF4) {
+    int cnt[kSumTiles];
+    const float* src[kSumTiles];
+    f4 acc[kSumTiles];
 #pragma unroll
-    for (int i = tid; i < kF4; i += kThreads) {
-      f4 acc = ld4(src + 4 * i);
-      int kb = 1;
-      for (; kb + 3 < cnt; kb += 4) {
-        const f4 x0 = ld4(src + kb * slot + 4 * i), x1 = ld4(src + (kb + 1) * slot + 4 * i);
-        const f4 x2 = ld4(src + (kb + 2) * slot + 4 * i), x3 = ld4(src + (kb + 3) * slot + 4 * i);
-        acc += x0;
-        acc += x1;
-        acc += x2;
-        acc += x3;
+    for (int jj = 0; jj < kSumTiles; ++jj) {
+      const int j = min(j0 + jj, j1 - 1);
+      cnt[jj] = j0 + jj >= j1 ? 0
+                : a.causal ? min(nkb - 1, min(S - 1, j * kQT + kQT - 1) / kBwdKeys) + 1
+                           : nkb;
+      src[jj] = a.part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D) + 4 * i;
+    }
+    for (int kb0 = 0; kb0 < need; kb0 += 4) {
+      f4 x[kSumTiles][4];
+#pragma unroll
+      for (int jj = 0; jj < kSumTiles; ++jj) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int kb = kb0 + k;
+          x[jj][k] = kb < cnt[jj] ? ld4(src[jj] + min(kb, cnt[jj] - 1) * slot) : zero4();
+        }
       }
-      for (; kb < cnt; ++kb) acc += ld4(src + kb * slot + 4 * i);
-      acc *= a.scale;
-      // Fragment order: register r of float4 i is query q0 + 16 mm + 4 g + r, dim 16 dt + lo.
-      const int lane = i & 63, md = i >> 6, dt = md % kDT, mm = md / kDT;
-      const int lo = lane & 15, g = lane >> 4;
+#pragma unroll
+      for (int jj = 0; jj < kSumTiles; ++jj) {
+        if (kb0 < cnt[jj]) acc[jj] = kb0 == 0 ? x[jj][0] : acc[jj] + x[jj][0];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) {
+          if (kb0 + k < cnt[jj]) acc[jj] += x[jj][k];
+        }
+      }
+    }
+    // Fragment order: register r of float4 i is query q0 + 16 mm + 4 g + r, dim 16 dt + lo.
+    const int lane = i & 63, md = i >> 6, dt = md % kDT, mm = md / kDT;
+    const int lo = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int jj = 0; jj < kSumTiles; ++jj) {
+      if (j0 + jj >= j1) break;
+      const f4 r4 = acc[jj] * a.scale;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int q = q0 + 16 * mm + 4 * g + r;
-        if (q < S) dq_bh[q * row_stride + 16 * dt + lo] = acc[r];
+        const int q = (j0 + jj) * kQT + 16 * mm + 4 * g + r;
+        if (q < S) dq_bh[q * row_stride + 16 * dt + lo] = r4[r];
       }
     }
   }
