@@ -221,6 +221,34 @@ def test_backward_is_deterministic(orc, cuda, causal, path, dq_sum):
         assert torch.equal(bits(o2), ob1)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_side_streams(orc, cuda, causal, dq_sum):
+    """Every launch goes on the caller's current stream (src/cuda.rs launches on candle's stream):
+    two forward + backward passes on two side streams, their launches interleaved and their
+    backwards in flight together (each with its own workspace), equal the same passes on the
+    default stream bit for bit."""
+    b, s, h, d = 4, 240, 6, 64
+    say(f"side streams causal={causal} {dq_sum}")
+    inputs = [tuple(torch.from_numpy(a).to(cuda) for a in orc.seeded_qkv_inputs(b, h, s, seed=sd, d=d))
+              for sd in (11, 12)]
+    want = [run("fused_qkv", x, w, h, d, causal, 0.125) for x, w in inputs]
+    streams = [torch.cuda.Stream(cuda), torch.cuda.Stream(cuda)]
+    xs, outs = [], []
+    for (x, _), st in zip(inputs, streams):
+        st.wait_stream(torch.cuda.current_stream(cuda))
+        with torch.cuda.stream(st):
+            xg = x.detach().clone().requires_grad_(True)
+            xs.append(xg)
+            outs.append(cfa.fused_attention_qkv(xg, h, 0.125, causal))
+    for (_, w), xg, o, st in zip(inputs, xs, outs, streams):
+        with torch.cuda.stream(st):
+            (o * w).sum().backward()
+    torch.cuda.synchronize()
+    for (o_want, g_want), xg, o in zip(want, xs, outs):
+        assert torch.equal(bits(o.detach()), bits(o_want))
+        assert torch.equal(bits(xg.grad), bits(g_want))
+
+
 # --- edge cases ------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("causal", [False, True])
