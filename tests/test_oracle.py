@@ -9,7 +9,9 @@ sign, a transposed operand, a missing scale, a wrong causal side) fails at least
     and dQ = dK = 0;
   - invariants: sum_j dK_j = 0 and sum_j dV_j = sum_i dO_i per (b, h); L >= row max; O in the
     convex hull of the value rows;
-  - the planted-mistake test shows those invariants reject a backward with one term dropped.
+  - the planted-mistake test shows those invariants reject a backward with one term dropped;
+    tests/test_oracle_mutants.py plants ten such mistakes in a numpy restatement and shows each
+    fails at least one of these checks.
 """
 from __future__ import annotations
 
