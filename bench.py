@@ -138,9 +138,19 @@ def main() -> int:
         bwd()
     torch.cuda.synchronize()
 
-    def timed(fn, n):
+    # roctx ranges name the timed windows (the reference brackets them with cuProfilerStart /
+    # Stop for an nsys capture range, examples/compare.rs:261-277); `rocprofv3 --marker-trace`
+    # records them. torch.cuda.nvtx is roctx on ROCm.
+    def range_push(name):
+        torch.cuda.nvtx.range_push(name)
+
+    def range_pop():
+        torch.cuda.nvtx.range_pop()
+
+    def timed(fn, n, name):
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        range_push(name)
         t0 = time.perf_counter()
         e0.record(stream)
         for _ in range(n):
@@ -148,12 +158,13 @@ def main() -> int:
         e1.record(stream)
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3 / n
+        range_pop()
         return e0.elapsed_time(e1) / n, wall
 
     K = max(args.steps, 1)
     step = lambda: (fwd(), bwd())  # noqa: E731
-    fwd_bwd_ms, fwd_bwd_wall = timed(step, K)
-    fwd_ms, _ = timed(fwd, K)
+    fwd_bwd_ms, fwd_bwd_wall = timed(step, K, "fattn timed fwd+bwd")
+    fwd_ms, _ = timed(fwd, K, "fattn timed fwd")
     log(f"bench: fwd+bwd {fwd_bwd_ms:.4f} ms (wall {fwd_bwd_wall:.4f}), fwd {fwd_ms:.4f} ms")
 
     # Per-kernel durations: K more steps, back to back as above, with the backward launched as
@@ -166,6 +177,7 @@ def main() -> int:
         kernels.append(("bwd_dq", dq_k))
     marks = []
     torch.cuda.synchronize()
+    range_push("fattn kernel-level steps")
     for _ in range(K):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)]
         ev[0].record(stream)
@@ -174,6 +186,7 @@ def main() -> int:
             ev[i + 1].record(stream)
         marks.append(ev)
     torch.cuda.synchronize()
+    range_pop()
     kus = {name: statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in marks) * 1e3
            for i, (name, _) in enumerate(kernels)}
     steps_us = statistics.mean(ev[0].elapsed_time(ev[-1]) for ev in marks) * 1e3
