@@ -8,12 +8,22 @@ config 2's synthetic inputs (qkv [64, 240, 1152] ~ N(0, 1) and dout [64, 240, 38
 by a CPU torch generator seeded 0, the reference's published inputs), resident in HBM before the
 timed region. The op-level C ABI is called with preallocated outputs on torch's current stream.
 
+Configs 3-5 (causal, long causal, strided views) are timed too, as extra keys of the same line
+(`configs`): op-level forward and forward+backward, and each kernel on its own.
+
 Prints ONE JSON line. `--gpus N` with N > 1 exits: this build runs on one GPU.
+
+`--traffic-from FETCH_CSV WRITE_CSV` does not touch a GPU: it turns two `rocprofv3 --pmc
+FETCH_SIZE` / `--pmc WRITE_SIZE` counter files of a `--calibrate-copy` run into
+profiles/traffic.json (HBM bytes per launch, scaled by the 256 MiB copy's counters, tagged with
+the sha256 of the libfattn.so that was measured).
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
+import hashlib
 import json
 import os
 import statistics
@@ -29,8 +39,20 @@ for p in (str(REPO), str(REPO / "candle-fused-attn_amd")):
 METRIC = "fwd & fwd+bwd ms at b64 h6 s240 d64 fp32; % of fp32 MFMA peak"
 PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak (public spec)
 PEAK_HBM_GBS = 8000.0
-B, H, S, D = 64, 6, 240, 64
 SCALE = 0.125
+TRAFFIC = REPO / "profiles" / "traffic.json"
+LIB = REPO / "candle-fused-attn_amd" / "lib" / "libfattn.so"
+COPY_KIB = 256 * 1024            # the --calibrate-copy kernel moves 256 MiB each way
+KERNEL_NAMES = {"fwd": "fwd_kernel<64, 128, 32, 3>", "bwd_main": "bwd_split_kernel<64>",
+                "bwd_dq": "dq_kernel<64>"}
+
+# The BASELINE.json configurations this bench times: (name, kind, b, h, s, causal, seed, std).
+CONFIGS = {
+    2: ("config 2", "qkv", 64, 6, 240, False, 0, 1.0),
+    3: ("config 3", "qkv", 64, 6, 240, True, 0, 1.0),
+    4: ("config 4", "qkv", 8, 12, 2048, True, 2, 1.0),
+    5: ("config 5", "strided", 16, 16, 1024, False, 3, 2.0),
+}
 
 
 def flops(b, h, s, d, causal):
@@ -42,22 +64,266 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def lib_sha256() -> str | None:
+    try:
+        return hashlib.sha256(LIB.read_bytes()).hexdigest()[:16]
+    except OSError:
+        return None
+
+
+class Workload:
+    """One configuration's operands, resident on the device, and closures over the C ABI: the
+    op-level forward and backward (what a step runs) and the kernel-level launches of the same
+    kernels on the same views (to time each kernel)."""
+
+    def __init__(self, torch, L, _lib, dev, cfg: int, d: int = 64):
+        import ctypes as C
+        name, kind, b, h, s, causal, seed, std = CONFIGS[cfg]
+        self.cfg, self.name, self.kind = cfg, name, kind
+        self.b, self.h, self.s, self.d, self.causal = b, h, s, d, causal
+        self.seed, self.std = seed, std
+        P = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+        ci = int(causal)
+        st = torch.cuda.current_stream(dev)
+        sp = C.c_void_p(st.cuda_stream)
+        self.stream = st
+        hd = h * d
+        if kind == "qkv":
+            if cfg in (2, 3):
+                # Exactly as bench/compare.py:496-503 draws them: qkv, then dout, on the CPU.
+                g = torch.Generator().manual_seed(seed)
+                self.qkv_cpu = torch.randn(b, s, 3 * hd, generator=g)
+                self.dout_cpu = torch.randn(b, s, hd, generator=g)
+                qkv, dout = self.qkv_cpu.to(dev), self.dout_cpu.to(dev)
+            else:
+                g = torch.Generator(device=dev).manual_seed(seed)
+                qkv = torch.randn(b, s, 3 * hd, generator=g, device=dev)
+                dout = torch.randn(b, s, hd, generator=g, device=dev)
+            out = torch.empty(b, s, hd, device=dev)
+            dqkv = torch.empty_like(qkv)
+            shape, strides = _lib.arr(qkv.shape), _lib.arr(qkv.stride())
+            gshape, gstrides = _lib.arr(dout.shape), _lib.arr(dout.stride())
+            base = qkv.data_ptr()
+            views = [C.c_void_p(base + i * hd * 4) for i in range(3)]
+            vst = [_lib.arr([s * 3 * hd, d, 3 * hd])] * 3
+            gst = _lib.arr([s * hd, d, hd])
+            dout_p = P(dout)
+        else:
+            # q, k, v = transpose(1, 2) of [b, s, h, d] buffers ~ N(0, std^2), read in place
+            # (strides [s h d, d, h d, 1]); dO [b, h, s, d] ~ N(0, 1).
+            g = torch.Generator(device=dev).manual_seed(seed)
+            bufs = [torch.randn(b, s, h, d, generator=g, device=dev) * std for _ in range(3)]
+            do = torch.randn(b, h, s, d, generator=g, device=dev)
+            qkv, dout = bufs, do
+            out = torch.empty(b, s, h, d, device=dev)
+            dqkv = torch.empty(b, s, 3, h, d, device=dev)
+            bshape = _lib.arr([b, h, s, d])
+            bstride = _lib.arr([s * h * d, d, h * d, 1])
+            graw = do.transpose(1, 2)  # the gradient of the raw [b, s, h, d] output
+            gshape, gstrides = _lib.arr(graw.shape), _lib.arr(graw.stride())
+            views = [P(t) for t in bufs]
+            vst = [_lib.arr([s * h * d, d, h * d])] * 3
+            gst = _lib.arr([h * s * d, s * d, d])
+            dout_p = P(do)
+        lse = torch.empty(b, h, s, device=dev)
+        ws_bytes = int(L.fattn_bwd_workspace_bytes(b, h, s, d))
+        ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        self.split = ws_bytes >= int(L.fattn_bwd_workspace_split_bytes(b, h, s, d))
+        self.tensors = (qkv, dout, out, lse, dqkv, ws)  # kept alive
+        self.out, self.lse, self.dqkv = out, lse, dqkv
+
+        if kind == "qkv":
+            def fwd():
+                _lib.check(L.fattn_qkv_forward(P(qkv), 0, shape, strides, h, SCALE, ci, P(out),
+                                               P(lse), sp))
+
+            def bwd():
+                _lib.check(L.fattn_qkv_backward(P(qkv), 0, shape, strides, h, SCALE, ci, P(out),
+                                                P(lse), dout_p, 0, gshape, gstrides, P(dqkv),
+                                                P(ws), ws_bytes, sp))
+        else:
+            args = []
+            for t in bufs:
+                args += [P(t), 0, bshape, bstride]
+
+            def fwd():
+                _lib.check(L.fattn_forward(*args, SCALE, ci, P(out), P(lse), sp))
+
+            def bwd():
+                _lib.check(L.fattn_backward(*args, SCALE, ci, P(out), P(lse), dout_p, 0, gshape,
+                                            gstrides, P(dqkv), P(ws), ws_bytes, sp))
+
+        def fwd_k():
+            _lib.check(L.fattn_fwd_f32_d64(*views, P(out), P(lse), b, h, s, d, SCALE, ci, *vst,
+                                           sp))
+
+        def prep_k():
+            _lib.check(L.fattn_bwd_prep_f32_d64(P(out), dout_p, gst, P(ws), ws_bytes, b, h, s, d,
+                                                sp))
+
+        def main_k():
+            _lib.check(L.fattn_bwd_main_f32_d64(*views, P(out), dout_p, P(lse), P(dqkv), P(ws),
+                                                ws_bytes, b, h, s, d, SCALE, ci, *vst, gst, sp))
+
+        def dq_k():
+            _lib.check(L.fattn_bwd_dq_f32_d64(P(dqkv), P(ws), ws_bytes, b, h, s, d, SCALE, ci,
+                                              sp))
+
+        self.fwd, self.bwd = fwd, bwd
+        # With a split workspace at d 64 step 1 launches nothing (step 2 computes D itself, and
+        # its last workgroups sum dQ tiles); step 3 sums the tiles those left.
+        self.kernels = [("fwd", fwd_k), ("bwd_prep", prep_k), ("bwd_main", main_k)]
+        if self.split:
+            self.kernels.append(("bwd_dq", dq_k))
+
+    def step(self):
+        self.fwd()
+        self.bwd()
+
+    def flops(self):
+        return flops(self.b, self.h, self.s, self.d, self.causal)
+
+
+def event_steps(torch, stream, fn, n):
+    """n calls of fn back to back, a HIP event on the launch stream before the first and after
+    each: (mean ms per call over all n, the per-call ms list, host wall ms per call)."""
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for i in range(n):
+        fn()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / n
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
+    return ev[0].elapsed_time(ev[n]) / n, per, wall
+
+
+def kernel_steps(torch, stream, kernels, n):
+    """n steps launched kernel by kernel, back to back, a HIP event between every two launches:
+    mean us per kernel, and per step."""
+    marks = []
+    torch.cuda.synchronize()
+    for _ in range(n):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)]
+        ev[0].record(stream)
+        for i, (_, fn) in enumerate(kernels):
+            fn()
+            ev[i + 1].record(stream)
+        marks.append(ev)
+    torch.cuda.synchronize()
+    kus = {name: statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in marks) * 1e3
+           for i, (name, _) in enumerate(kernels)}
+    kus["step"] = statistics.mean(ev[0].elapsed_time(ev[-1]) for ev in marks) * 1e3
+    return kus
+
+
+def traffic_entry():
+    """roofline.traffic from profiles/traffic.json: the measured HBM bytes of step 2 when that file
+    was measured on this very libfattn.so (same sha256), else null (stale; the old figure is kept
+    under another key)."""
+    sha = lib_sha256()
+    try:
+        t = json.loads(TRAFFIC.read_text())
+    except (OSError, ValueError):
+        return {"traffic": None, "lib_sha256": sha, "traffic_lib_sha256": None}
+    tsha = t.get("lib_sha256")
+    cur = tsha is not None and tsha == sha
+    res = {"traffic": t.get("bwd_main_bytes") if cur else None, "lib_sha256": sha,
+           "traffic_lib_sha256": tsha}
+    if not cur:
+        res["traffic_stale_bytes"] = t.get("bwd_main_bytes")
+    return res
+
+
+def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
+    """profiles/traffic.json from two counter runs of `bench.py --calibrate-copy` (one counter
+    each): per kernel the mean FETCH_SIZE / WRITE_SIZE over its launches, in KiB, each scaled by
+    what the same counter reads for the 256 MiB device copy (bytes it is known to move)."""
+    def load(path, counter):
+        vals: dict[str, list[float]] = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") == counter:
+                    vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return vals
+
+    fetch, write = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+    copy = [k for k in fetch if "copyBuffer" in k]
+    if not copy:
+        print("bench.py: no copy kernel in the counter files (run with --calibrate-copy)",
+              file=sys.stderr)
+        return 1
+    cf, cw = fetch[copy[0]][0], write[copy[0]][0]
+    sf, sw = COPY_KIB / cf, COPY_KIB / cw
+    out = {"workload": "config 2: qkv [64, 240, 1152] h6 d64 non-causal",
+           "lib_sha256": lib_sha256(), "copy_calibration_kib": COPY_KIB,
+           "copy_fetch_kib": round(cf, 1), "copy_write_kib": round(cw, 1),
+           "scale_fetch": round(sf, 5), "scale_write": round(sw, 5)}
+    for key, pat in KERNEL_NAMES.items():
+        names = [n for n in fetch if pat in n]
+        if not names:
+            continue
+        fr, wr = statistics.mean(fetch[names[0]]), statistics.mean(write[names[0]])
+        fb, wb = round(fr * 1024 * sf), round(wr * 1024 * sw)
+        out[key] = {"fetch_kib_raw": round(fr, 2), "write_kib_raw": round(wr, 2),
+                    "fetch_bytes": fb, "write_bytes": wb, "bytes": fb + wb}
+    out["bwd_main_bytes"] = out.get("bwd_main", {}).get("bytes")
+    out["fwd_bytes"] = out.get("fwd", {}).get("bytes")
+    TRAFFIC.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out, indent=1))
+    return 0
+
+
+def time_extra(torch, w: Workload, steps: int, warmup: int) -> dict:
+    """Op-level forward and forward+backward ms, and each kernel's us, of one extra config."""
+    for _ in range(warmup):
+        w.step()
+    fb_ms, _, _ = event_steps(torch, w.stream, w.step, steps)
+    f_ms, _, _ = event_steps(torch, w.stream, w.fwd, steps)
+    kus = kernel_steps(torch, w.stream, w.kernels, steps)
+    f_fwd, f_bwd = w.flops()
+    bwd_us = kus.get("bwd_prep", 0.0) + kus["bwd_main"] + kus.get("bwd_dq", 0.0)
+    return {
+        "workload": f"{w.kind} b{w.b} h{w.h} s{w.s} d{w.d} "
+                    + ("causal" if w.causal else "non-causal")
+                    + (f", inputs ~N(0, {w.std ** 2:g})" if w.std != 1.0 else ""),
+        "fwd_ms": round(f_ms, 5), "fwd_bwd_ms": round(fb_ms, 5),
+        "fwd_bwd_tflops": round((f_fwd + f_bwd) / (fb_ms * 1e-3) / 1e12, 3),
+        "kernels_us": {k: round(v, 2) for k, v in kus.items()},
+        "bwd_main_frac": round(f_bwd / (kus["bwd_main"] * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "bwd_steps_frac": round(f_bwd / (bwd_us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "fwd_kernel_frac": round(f_fwd / (kus["fwd"] * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "dq_sum": "split" if w.split else "turns",
+        "steps": steps, "warmup": warmup,
+    }
+
+
 def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__)
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     # MI355X raises its clocks over the first ~20 ms of sustained work (a kernel trace shows the
-    # forward going from 71 to 58 us per call over that time); 200 warm-up steps (~45 ms) put
-    # the timed steps at the steady state a training loop runs at.
+    # forward going from 71 to 58 us per call over that time); the default 200 warm-up steps
+    # (~45 ms) put the timed steps at the steady state a training loop runs at. The line reports
+    # the first and last five timed steps, so a run with fewer warm-ups shows its ramp.
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--causal", action="store_true", help="config 3 instead of config 2")
+    ap.add_argument("--causal", action="store_true", help="config 3 as the main workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-accuracy", action="store_true", help="skip the fp64 scoring")
+    ap.add_argument("--no-extra", action="store_true", help="skip timing configs 3-5")
+    ap.add_argument("--extra-steps", type=int, default=20)
     ap.add_argument("--cpu-threads", type=int, default=None)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 256 MiB device-to-device copy (a kernel of known traffic, "
                          "to scale rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic.json from two counter files and exit (no GPU)")
     args = ap.parse_args()
+    if args.traffic_from:
+        return summarize_traffic(*args.traffic_from)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
               "(the op shards over (batch, head) with no communication; see DESIGN.md)",
@@ -75,140 +341,56 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     L = _lib.lib()
-    causal = bool(args.causal)
-
-    # Inputs exactly as bench/compare.py:496-503 draws them.
-    g = torch.Generator().manual_seed(0)
-    qkv_cpu = torch.randn(B, S, 3 * H * D, generator=g)
-    dout_cpu = torch.randn(B, S, H * D, generator=g)
-    qkv = qkv_cpu.to(dev)
-    dout = dout_cpu.to(dev)
-    out = torch.empty(B, S, H * D, device=dev)
-    lse = torch.empty(B, H, S, device=dev)
-    dqkv = torch.empty_like(qkv)
-    ws_bytes = int(L.fattn_bwd_workspace_bytes(B, H, S, D))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream(dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    shape, strides = _lib.arr(qkv.shape), _lib.arr(qkv.stride())
-    gshape, gstrides = _lib.arr(dout.shape), _lib.arr(dout.stride())
-    ci = int(causal)
-
-    def fwd():
-        _lib.check(L.fattn_qkv_forward(P(qkv), 0, shape, strides, H, SCALE, ci, P(out), P(lse),
-                                       sp))
-
-    def bwd():
-        _lib.check(L.fattn_qkv_backward(P(qkv), 0, shape, strides, H, SCALE, ci, P(out), P(lse),
-                                        P(dout), 0, gshape, gstrides, P(dqkv), P(ws), ws_bytes,
-                                        sp))
-
-    # Kernel-level views of the same operands, to time each kernel on its own.
-    qst = _lib.arr([S * 3 * H * D, D, 3 * H * D])
-    gst = _lib.arr([S * H * D, D, H * D])
-    base = qkv.data_ptr()
-    qp, kp, vp = (ctypes.c_void_p(base + i * H * D * 4) for i in range(3))
-
-    def prep_k():
-        _lib.check(L.fattn_bwd_prep_f32_d64(P(out), P(dout), gst, P(ws), ws_bytes, B, H, S, D,
-                                            sp))
-
-    def main_k():
-        _lib.check(L.fattn_bwd_main_f32_d64(qp, kp, vp, P(out), P(dout), P(lse), P(dqkv), P(ws),
-                                            ws_bytes, B, H, S, D, SCALE, ci, qst, qst, qst, gst,
-                                            sp))
-
-    def dq_k():
-        _lib.check(L.fattn_bwd_dq_f32_d64(P(dqkv), P(ws), ws_bytes, B, H, S, D, SCALE, ci, sp))
-
-    split = ws_bytes >= int(L.fattn_bwd_workspace_split_bytes(B, H, S, D))
+    main_cfg = 3 if args.causal else 2
+    w = Workload(torch, L, _lib, dev, main_cfg)
+    B, H, S, D, causal = w.b, w.h, w.s, w.d, w.causal
 
     if args.calibrate_copy:
-        src = torch.ones(64 * 1024 * 1024, device=dev)   # 256 MiB
+        src = torch.ones(COPY_KIB * 256, device=dev)   # 256 MiB of f32
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    log(f"bench: config {'3 (causal)' if causal else '2'} b{B} h{H} s{S} d{D}; "
-        f"warmup {args.warmup}, steps {args.steps}")
+    log(f"bench: config {main_cfg} b{B} h{H} s{S} d{D}; warmup {args.warmup}, "
+        f"steps {args.steps}")
     for _ in range(max(args.warmup, 1)):
-        fwd()
-        bwd()
+        w.step()
     torch.cuda.synchronize()
 
     # roctx ranges name the timed windows (the reference brackets them with cuProfilerStart /
     # Stop for an nsys capture range, examples/compare.rs:261-277); `rocprofv3 --marker-trace`
     # records them. torch.cuda.nvtx is roctx on ROCm.
-    def range_push(name):
-        torch.cuda.nvtx.range_push(name)
-
-    def range_pop():
-        torch.cuda.nvtx.range_pop()
-
-    def timed(fn, n, name):
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        range_push(name)
-        t0 = time.perf_counter()
-        e0.record(stream)
-        for _ in range(n):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) * 1e3 / n
-        range_pop()
-        return e0.elapsed_time(e1) / n, wall
-
     K = max(args.steps, 1)
-    step = lambda: (fwd(), bwd())  # noqa: E731
-    fwd_bwd_ms, fwd_bwd_wall = timed(step, K, "fattn timed fwd+bwd")
-    fwd_ms, _ = timed(fwd, K, "fattn timed fwd")
-    log(f"bench: fwd+bwd {fwd_bwd_ms:.4f} ms (wall {fwd_bwd_wall:.4f}), fwd {fwd_ms:.4f} ms")
+    torch.cuda.nvtx.range_push("fattn timed fwd+bwd")
+    fwd_bwd_ms, per_step, fwd_bwd_wall = event_steps(torch, w.stream, w.step, K)
+    torch.cuda.nvtx.range_pop()
+    torch.cuda.nvtx.range_push("fattn timed fwd")
+    fwd_ms, _, _ = event_steps(torch, w.stream, w.fwd, K)
+    torch.cuda.nvtx.range_pop()
+    n5 = min(5, K)
+    first5, last5 = statistics.mean(per_step[:n5]), statistics.mean(per_step[-n5:])
+    log(f"bench: fwd+bwd {fwd_bwd_ms:.4f} ms (wall {fwd_bwd_wall:.4f}; first {n5} steps "
+        f"{first5:.4f}, last {n5} {last5:.4f}), fwd {fwd_ms:.4f} ms")
 
     # Per-kernel durations: K more steps, back to back as above, with the backward launched as
-    # its kernel-level steps (the same kernels on the same arguments as fattn_qkv_backward) and a
-    # HIP event on the launch stream between every two launches.
-    # With a split workspace at d 64 step 1 launches nothing (step 2 computes D itself, and its
-    # last workgroups sum dQ tiles); step 3 sums the tiles those left.
-    kernels = [("fwd", fwd), ("bwd_prep", prep_k), ("bwd_main", main_k)]
-    if split:
-        kernels.append(("bwd_dq", dq_k))
-    marks = []
-    torch.cuda.synchronize()
-    range_push("fattn kernel-level steps")
-    for _ in range(K):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)]
-        ev[0].record(stream)
-        for i, (_, fn) in enumerate(kernels):
-            fn()
-            ev[i + 1].record(stream)
-        marks.append(ev)
-    torch.cuda.synchronize()
-    range_pop()
-    kus = {name: statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in marks) * 1e3
-           for i, (name, _) in enumerate(kernels)}
-    steps_us = statistics.mean(ev[0].elapsed_time(ev[-1]) for ev in marks) * 1e3
+    # its kernel-level steps (the same kernels on the same arguments as the op-level backward)
+    # and a HIP event on the launch stream between every two launches.
+    torch.cuda.nvtx.range_push("fattn kernel-level steps")
+    kus = kernel_steps(torch, w.stream, w.kernels, K)
+    torch.cuda.nvtx.range_pop()
     fwd_us, prep_us, main_us = kus["fwd"], kus.get("bwd_prep", 0.0), kus["bwd_main"]
     dq_us = kus.get("bwd_dq", 0.0)
     log(f"bench: kernels fwd {fwd_us:.1f} us, prep {prep_us:.1f} us, bwd main {main_us:.1f} us, "
-        f"dq sum {dq_us:.1f} us ({'split' if split else 'turns'}); step {steps_us:.1f} us")
+        f"dq sum {dq_us:.1f} us ({'split' if w.split else 'turns'}); step {kus['step']:.1f} us")
 
-    f_fwd, f_bwd = flops(B, H, S, D, causal)
+    f_fwd, f_bwd = w.flops()
     fwd_tflops = f_fwd / (fwd_ms * 1e-3) / 1e12
     total_tflops = (f_fwd + f_bwd) / (fwd_bwd_ms * 1e-3) / 1e12
     main_tflops = f_bwd / (main_us * 1e-6) / 1e12
     bwd_steps_tflops = f_bwd / ((prep_us + main_us + dq_us) * 1e-6) / 1e12
     fwdk_tflops = f_fwd / (fwd_us * 1e-6) / 1e12
-
-    traffic = None
-    tfile = REPO / "profiles" / "traffic.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("bwd_main_bytes")
-        except (OSError, ValueError):
-            traffic = None
+    traffic = traffic_entry()
 
     result = {
         "metric": METRIC,
@@ -224,8 +406,8 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": ("qkv path forward+backward, qkv [64, 240, 1152] (h 6, d 64) and dout "
-                         "[64, 240, 384] ~ N(0,1) seed 0, scale 1/8, "
+            "workload": (f"qkv path forward+backward, qkv [{B}, {S}, {3 * H * D}] (h {H}, d {D}) "
+                         f"and dout [{B}, {S}, {H * D}] ~ N(0,1) seed 0, scale 1/8, "
                          + ("causal (config 3)" if causal else "non-causal (config 2)")),
             "b": B, "h": H, "s": S, "d": D, "causal": causal,
             "entry": "fattn_qkv_forward + fattn_qkv_backward",
@@ -233,23 +415,25 @@ def main() -> int:
         "fwd_ms": round(fwd_ms, 5),
         "fwd_bwd_ms": round(fwd_bwd_ms, 5),
         "fwd_bwd_wall_ms": round(fwd_bwd_wall, 5),
+        "fwd_bwd_first5_ms": round(first5, 5),
+        "fwd_bwd_last5_ms": round(last5, 5),
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_bwd_tflops": round(total_tflops, 3),
         "frac_fp32_peak": round(total_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
         "kernels_us": {"fwd": round(fwd_us, 2), "bwd_prep": round(prep_us, 2),
                        "bwd_main": round(main_us, 2), "bwd_dq": round(dq_us, 2),
-                       "step": round(steps_us, 2)},
-        "dq_sum": "split" if split else "turns",
+                       "step": round(kus["step"], 2)},
+        "dq_sum": "split" if w.split else "turns",
         "roofline": {
             "kernel": ("bwd_split_kernel<64> (fattn_bwd_main_f32_d64, split; its last "
-                       "workgroups sum dQ tiles)" if split
+                       "workgroups sum dQ tiles)" if w.split
                        else "bwd_kernel<false, 64> (fattn_bwd_main_f32_d64, turns)"),
             "bound": "mfma",
             "achieved": round(main_tflops, 3),
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(main_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
-            "traffic": traffic,
+            **traffic,
             "flops_per_launch": f_bwd,
             "bwd_steps_1_3_achieved": round(bwd_steps_tflops, 3),
             "fwd_kernel_achieved": round(fwdk_tflops, 3),
@@ -257,37 +441,49 @@ def main() -> int:
         },
     }
 
+    if not args.no_extra:
+        extra = {}
+        for cfg in (2, 3, 4, 5):
+            if cfg == main_cfg:
+                continue
+            xw = Workload(torch, L, _lib, dev, cfg)
+            extra[f"config{cfg}"] = time_extra(torch, xw, max(args.extra_steps, 1), 3)
+            log(f"bench: {CONFIGS[cfg][0]}: {json.dumps(extra[f'config{cfg}'])}")
+            del xw
+            torch.cuda.empty_cache()
+        result["configs"] = extra
+
     if not args.no_accuracy:
         from oracle import oracle as orc
-        fwd()
-        bwd()
+        w.step()
         torch.cuda.synchronize()
-        first = dqkv.clone()
-        bwd()
+        first = w.dqkv.clone()
+        w.bwd()
         torch.cuda.synchronize()
-        rerun_equal = bool(torch.equal(first.view(torch.int32), dqkv.view(torch.int32)))
+        rerun_equal = bool(torch.equal(first.view(torch.int32), w.dqkv.view(torch.int32)))
         t0 = time.perf_counter()
-        x, dd = qkv_cpu.numpy(), dout_cpu.numpy()
+        x, dd = w.qkv_cpu.numpy(), w.dout_cpu.numpy()
         ro, rl = orc.qkv_forward(x, H, SCALE, causal, dtype=np.float64)
         rg = orc.qkv_backward(x, H, SCALE, causal, ro, rl, dd, dtype=np.float64)
-        go, gg = out.cpu().numpy(), dqkv.cpu().numpy()
+        go, gg, gl = w.out.cpu().numpy(), w.dqkv.cpu().numpy(), w.lse.cpu().numpy()
         acc = {"o": orc.rel_fro(go, ro)}
         for name, a, r in zip(("dq", "dk", "dv"), np.split(gg, 3, axis=-1),
                               np.split(rg, 3, axis=-1)):
             acc[name] = orc.rel_fro(a, r)
         result["accuracy"] = {
             "normwise_vs_fp64": {k: float(f"{v:.3e}") for k, v in acc.items()},
+            "lse_max_abs_vs_fp64": float(f"{orc.max_abs(gl, rl):.3e}"),
             "tolerance": 2e-6,
             "within_tolerance": all(v <= 2e-6 for v in acc.values()),
             "bitwise_rerun": rerun_equal,
         }
-        log(f"bench: accuracy {acc} (fp64 scoring {time.perf_counter() - t0:.1f} s), "
-            f"bitwise rerun {rerun_equal}")
+        log(f"bench: accuracy {acc}, L max-abs {orc.max_abs(gl, rl):.2e} "
+            f"(fp64 scoring {time.perf_counter() - t0:.1f} s), bitwise rerun {rerun_equal}")
 
     if not args.no_cpu:
         from oracle import oracle as orc
         threads = args.cpu_threads or orc.default_threads()
-        x, dd = qkv_cpu.numpy(), dout_cpu.numpy()
+        x, dd = w.qkv_cpu.numpy(), w.dout_cpu.numpy()
 
         def cpu_step(xx, gg, thr):
             o_, l_ = orc.qkv_forward(xx, H, SCALE, causal, dtype=np.float32, threads=thr)
@@ -318,7 +514,7 @@ def main() -> int:
             "unit": "ms",
             "cores": threads,
             "kind": "port",
-            "sample": (f"full config {'3' if causal else '2'} forward+backward, median of "
+            "sample": (f"full config {main_cfg} forward+backward, median of "
                        f"{len(ts)} after 1 warm-up, OpenMP over (b, h) on {threads} threads "
                        f"({cpu_name or 'unknown CPU'}, nproc {os.cpu_count()}); the C "
                        "restatement of the reference's composed CPU path (src/lib.rs:241-299)"),

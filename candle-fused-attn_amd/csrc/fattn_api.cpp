@@ -4,6 +4,7 @@
 // Validation runs before any HIP call, so a rejected call touches no device and needs none.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cstdint>
@@ -11,6 +12,7 @@
 #include <random>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "fattn.h"
 #include "fattn_internal.h"
@@ -574,6 +576,64 @@ int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
   const View g{grad + grad_offset, grad_strides[0], grad_strides[2], grad_strides[1]};
   return run_backward("fused_attention", qv, kv, vv, out, g, lse, dqkv, workspace,
                       workspace_bytes, b, h, s, d, scale, causal, stream);
+}
+
+// Test hook (not declared in include/fattn.h; tests/test_boundary.py calls it without a GPU): an
+// audit of step 2's dQ-sum schedule for one shape, on the host, with the scheduling functions the
+// kernel runs (fattn_internal.h). out[0]: summing workgroups in step 2's grid; out[1]: those with a
+// (b, h) to sum; out[2]: violations -- a summing workgroup waits for a key block that runs on
+// another XCD, or xcd_remap and item_xcd disagree, or a workgroup past the plan's range has a
+// target; out[3]: query tiles two workgroups would both sum; out[4]: query tiles summed.
+int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int causal,
+                             int64_t out[5]) {
+  if (!out || b <= 0 || h <= 0 || s <= 0 || b * h * s > (int64_t{1} << 26)) return FATTN_EINVAL;
+  const int BH = static_cast<int>(b * h);
+  const int nkb = static_cast<int>((s + fattn::kBwdKeys - 1) / fattn::kBwdKeys);
+  const int ntile = static_cast<int>((s + fattn::kBwdQueryTile - 1) / fattn::kBwdQueryTile);
+  const int total = nkb * BH;
+  const fattn::SumPlan plan = fattn::sum_plan(BH, nkb, ntile, static_cast<int>(d), causal);
+  const int64_t nsum = fattn::bwd_sum_blocks(b, h, s, static_cast<int>(d), causal);
+  int64_t targets = 0, bad = 0, twice = 0, covered = 0;
+  // xcd_remap is a permutation and item_xcd its inverse's XCD.
+  std::vector<char> seen(static_cast<size_t>(total), 0);
+  for (int id = 0; id < total; ++id) {
+    const int item = fattn::xcd_remap(id, total);
+    if (item < 0 || item >= total || seen[item]++ || fattn::item_xcd(item, total) != (id & 7)) {
+      ++bad;
+    }
+  }
+  std::vector<char> tile_done(static_cast<size_t>(BH) * ntile, 0);
+  for (int64_t i = 0; i < nsum + 64; ++i) {  // 64 past the grid: nothing may be assigned there
+    const int x = static_cast<int>(i & 7), m = static_cast<int>(i >> 3);
+    int bh = -1, j0 = -1;
+    if (!fattn::sum_target(plan, x, m, BH, causal, &bh, &j0)) continue;
+    if (i >= nsum || bh < 0 || bh >= BH || j0 < 0 || j0 >= ntile) {
+      ++bad;
+      continue;
+    }
+    ++targets;
+    const int j1 = std::min(ntile, j0 + fattn::kSumTiles);
+    // The key blocks the chunk waits for: all, or (causal) those holding a key <= its last query.
+    const int need = causal ? std::min<int64_t>(nkb - 1, std::min<int64_t>(s - 1,
+                                  int64_t{j1} * fattn::kBwdQueryTile - 1) / fattn::kBwdKeys) + 1
+                            : nkb;
+    for (int kb = 0; kb < need; ++kb) {
+      // Workgroup of key block kb of (b, h) bh: causal kb b h + bh (no remap); else the
+      // (b, h)-major item bh nkb + kb under xcd_remap.
+      const int xcd = causal ? ((kb * BH + bh) & 7) : fattn::item_xcd(bh * nkb + kb, total);
+      if (xcd != x) ++bad;
+    }
+    for (int j = j0; j < j1; ++j) {
+      if (tile_done[static_cast<size_t>(bh) * ntile + j]++) ++twice;
+      ++covered;
+    }
+  }
+  out[0] = nsum;
+  out[1] = targets;
+  out[2] = bad;
+  out[3] = twice;
+  out[4] = covered;
+  return 0;
 }
 
 int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,

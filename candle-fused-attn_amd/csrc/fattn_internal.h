@@ -1,8 +1,10 @@
 // Internal interface between the C-ABI layer (fattn_api.cpp) and the gfx950 kernels
-// (fattn_kernels.hip). Host-only types; no HIP headers needed to include it.
+// (fattn_kernels.hip), both compiled by hipcc. The scheduling functions below are __host__
+// __device__: the kernels and the host's grid sizes use the same code.
 #ifndef FATTN_INTERNAL_H
 #define FATTN_INTERNAL_H
 
+#include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -54,6 +56,52 @@ constexpr int kCtrlGuard = 32;
 // between launches and no stale or uninitialised value passes for a current one (but with a
 // 2^-64 chance). The summing workgroups poll at most kSumMaxBlocks arrival slots.
 constexpr int kSumMaxBlocks = 256;
+constexpr int kSumTiles = 3;  // query tiles per summing workgroup
+
+// Workgroups are dealt to the 8 XCDs round-robin (workgroup id % 8). xcd_remap gives each XCD a
+// contiguous range of logical items, so logical neighbours (the key blocks of one (b, h)) share
+// one L2: workgroup id runs item (id % 8) F + id / 8 with F = (total rounded down to a multiple
+// of 8) / 8; the last total % 8 items run as themselves.
+__host__ __device__ inline int xcd_remap(int id, int total) {
+  const int full = total & ~7;
+  if (id >= full) return id;
+  return (id & 7) * (full >> 3) + (id >> 3);
+}
+// The XCD that runs logical item `item` of xcd_remap (its inverse, taken mod 8).
+__host__ __device__ inline int item_xcd(int item, int total) {
+  const int full = total & ~7;
+  return item >= full ? (item & 7) : item / (full >> 3);
+}
+
+// The dQ sums in step 2's tail. `per` (b, h)s per XCD have every key block on that XCD: non-causal,
+// the (b, h)-major key blocks under xcd_remap, when F is a whole number of (b, h)s; causal, key
+// block kb of (b, h) is workgroup kb b h + bh, on XCD bh mod 8, when 8 divides b h. per = 0: no
+// sums (step 3 sums every tile). nchunk = chunks of kSumTiles query tiles per (b, h).
+struct SumPlan {
+  int per, nchunk;
+};
+__host__ __device__ inline SumPlan sum_plan(int BH, int nkb, int ntile, int d, int causal) {
+  SumPlan p{0, (ntile + kSumTiles - 1) / kSumTiles};
+  if (d > 64 || nkb > kSumMaxBlocks || BH <= 0) return p;
+  if (causal) {
+    p.per = BH % 8 == 0 ? BH / 8 : 0;
+  } else {
+    const int f = ((nkb * BH) & ~7) >> 3;
+    p.per = f > 0 && f % nkb == 0 ? f / nkb : 0;
+  }
+  return p;
+}
+// Summing workgroup m of XCD x (workgroup n_main + 8 m + x): the (b, h) it sums and its first
+// query tile. Non-causal: XCD x's (b, h)s one after the other; causal: tile-major (a tile's
+// contributors are the key blocks up to its last query, so the first tiles are complete first).
+// False for a workgroup with nothing to sum (m past the plan; never a (b, h) >= BH).
+__host__ __device__ inline bool sum_target(SumPlan p, int x, int m, int BH, int causal, int* bh,
+                                           int* j0) {
+  if (p.per <= 0 || m >= p.per * p.nchunk) return false;
+  *bh = causal ? x + 8 * (m % p.per) : x * p.per + m / p.nchunk;
+  *j0 = (causal ? m / p.per : m % p.nchunk) * kSumTiles;
+  return *bh < BH;
+}
 // Workgroups appended to step 2's grid for these sums (0: step 3 sums every tile).
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal);
 // Step 3's grid: one workgroup per query tile, or (with step 2's sums) at most 256 workgroups

@@ -246,14 +246,6 @@ __device__ __forceinline__ void load_lds4(const float* base, unsigned byte_off, 
                : "memory");
 }
 
-// Workgroups are handed to the 8 XCDs round-robin (id % 8). This permutation gives each XCD a
-// contiguous range of logical indices, so logical neighbours (same (b, h)) share one L2.
-__device__ __forceinline__ int xcd_remap(int id, int total) {
-  const int full = total & ~7;
-  if (id >= full) return id;
-  return (id & 7) * (full >> 3) + (id >> 3);
-}
-
 // s_waitcnt with vmcnt(n) and no lgkm / export wait (gfx9 encoding: vmcnt bits 3:0 and 15:14,
 // expcnt 6:4, lgkmcnt 11:8). Issued through the builtin, not inline asm, so that the compiler
 // knows which of its own loads have completed: otherwise it adds waits of its own at their first
@@ -624,7 +616,8 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
                                                        int* __restrict__ ctrl, int B, int H,
                                                        int S, int nturn) {
   constexpr int kLanes = D / 4;  // lanes per row
-  const int gtid = static_cast<int>(blockIdx.x) * kThreads + static_cast<int>(threadIdx.x);
+  // 64-bit: the grid holds up to b h s / (kThreads / kLanes) workgroups of kThreads threads.
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (gtid < nturn) turn[gtid] = 0;
   if (gtid < 64) ctrl[gtid] = 0;
   const int64_t rows = static_cast<int64_t>(B) * H * S;
@@ -692,12 +685,14 @@ struct BwdArgs {
   // split, D <= 64, null when step 3 sums every tile: per key block, the epoch of the launch
   // that finished it or'ed with its XCD; per query tile, the epoch of the launch that summed it
   // here; the workspace's record of this launch's epoch. Workgroups from n_main on sum tiles;
-  // n_main (the key blocks, rounded up to a multiple of 8) and the sums' layout below.
+  // n_main (the key blocks, rounded up to a multiple of 8) and the sums' plan (sum_plan, the same
+  // one the host sized the grid with).
   unsigned long long* arrive;
   unsigned long long* done;
   unsigned long long* epoch_slot;
   unsigned long long epoch;
   int n_main;
+  SumPlan plan;
   int* turn;
   int* ctrl;
   int B, H, S, nkb, ntile;
@@ -732,8 +727,9 @@ __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory")
 // wait_vm<n> waits for everything but the last n operations issued: stage 1's loads (turns) or the
 // partial's stores (split), the last operations before a tile's first barrier.
 
-// Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised.
-__device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
+// Spin until the turn counter reads `want`. Bounded: on timeout the guard word is raised and
+// the wait returns false (the turn never came: what the earlier key blocks summed is incomplete).
+__device__ __forceinline__ bool wait_turn(int* p, int want, int* guard) {
   int spins = 0;
   while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) {
     __builtin_amdgcn_s_sleep(2);
@@ -743,9 +739,10 @@ __device__ __forceinline__ void wait_turn(int* p, int want, int* guard) {
         ((spins & 63) == 0 &&
          __hip_atomic_load(guard, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) {
       __hip_atomic_store(guard, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
+      return false;
     }
   }
+  return true;
 }
 
 // Occupancy target: BWD_WAVES waves per SIMD (the kernel is latency-bound: with fewer, the
@@ -964,11 +961,17 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   // Stage 1 for the tile at q0p (waves with dQ tiles): wait for the turn (one lane polls), then
   // load. Exactly kStage1Loads load instructions are issued (rows past S read row S - 1, unused),
   // the last vector memory operations before the iteration's first barrier, so that barrier need
-  // not wait for them.
+  // not wait for them. A wait that gave up (the guard word is raised) makes the loaded sums NaN,
+  // so the tile's dQ reads NaN instead of a silently incomplete sum.
   constexpr int kStage1Loads = 4 * kNS * kDQ;
   auto load_sums = [&](int q0p, int pos, int seen, float (&sums)[kDQ][kNS][4]) {
     if (pos == 0 || !wave_dq) return;
-    if (lane == 0 && seen != pos) wait_turn(tp + q0p / kQT, pos, guard);
+    int gave_up = 0;
+    if (lane == 0 && seen != pos) gave_up = wait_turn(tp + q0p / kQT, pos, guard) ? 0 : 1;
+    // Every lane is active here (the tests above are wave-uniform): lane 0's result for all. Or'ed
+    // into the loaded bits, 0x7fc00000 makes any value a quiet NaN and 0 leaves it as it is (the
+    // loads stay unconditional, so their count before the barrier does not change).
+    const int poison = __builtin_amdgcn_readfirstlane(gave_up) ? 0x7fc00000 : 0;
     compiler_fence();
 #pragma unroll
     for (int j = 0; j < kDQ; ++j) {
@@ -977,7 +980,8 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int qi = min(q0p + 16 * m + 4 * g + r, S - 1);
-          sums[j][m][r] = ld_agent(dq_base + (16u * (w + 4 * j) + lo + qi * dq_row));
+          const float x = ld_agent(dq_base + (16u * (w + 4 * j) + lo + qi * dq_row));
+          sums[j][m][r] = __int_as_float(__float_as_int(x) | poison);
         }
       }
     }
@@ -1253,10 +1257,10 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // 2's tail, where the CUs run fewer and fewer key blocks; workgroups appended to step 2's grid do
 // its sums in that tail instead. In-order dispatch starts them only once every key block has been
 // dispatched. Workgroup n_main + 8 m + x (on XCD x: workgroups go to the XCDs round robin on
-// MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks xcd_remap puts on XCD x:
-// `per` consecutive (b, h)s from x per (the host enables this only when per is whole), kSumTiles
-// tiles per chunk, in the order their key blocks were dispatched (causal: see the mapping below;
-// a chunk then waits only for the key blocks its tiles need). Each key block, once its
+// MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks all run on XCD x
+// (sum_target: plan.per (b, h)s per XCD, kSumTiles tiles per chunk, in the order their key
+// blocks were dispatched; causal, a chunk waits only for the key blocks its tiles need; the host
+// sizes the grid from the same plan). Each key block, once its
 // partials are stored, writes the launch's epoch or'ed with its XCD to its arrival slot (agent
 // scope: written through to the coherence point, as the turn hand-over's counters). Wave 0 polls
 // the (b, h)'s slots (agent-scope loads) until every one holds this launch's epoch, sleeping
@@ -1269,21 +1273,14 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // gave up, only leaves work to step 3. Every poll ends: the key blocks have smaller workgroup
 // numbers on the same XCD, so they were dispatched before this workgroup and run to completion
 // whatever it does.
+// kSumTiles query tiles per summing workgroup: at config 2, 1, 2 or 15 were slower and 4 the same.
 constexpr int kSumPolls = 4096;
-constexpr int kSumTiles = 3;  // query tiles per summing workgroup (config 2: 1, 2, 15 slower; 4 same)
 template <int D>
 __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, unsigned* flag) {
   constexpr int kDT = D / 16, kF4 = kQT * D / 4;
   const int tid = threadIdx.x, BH = a.B * a.H, ntile = a.ntile, nkb = a.nkb;
-  const int nchunk = (ntile + kSumTiles - 1) / kSumTiles;
-  // Non-causal: the (b, h)s whose key blocks xcd_remap put on XCD x, one (b, h) after the other.
-  // Causal: key block kb of (b, h) is workgroup kb b h + bh, on XCD bh mod 8 when 8 divides b h;
-  // the chunks go tile-major (a tile's contributors are the key blocks up to its last query, so
-  // the first tiles are complete first).
-  const int per = a.causal ? BH / 8 : ((a.n_main & ~7) >> 3) / nkb;
-  if (m >= per * nchunk) return;
-  const int bh = a.causal ? x + 8 * (m % per) : x * per + m / nchunk;
-  const int j0 = (a.causal ? m / per : m % nchunk) * kSumTiles;
+  int bh, j0;
+  if (!sum_target(a.plan, x, m, BH, a.causal, &bh, &j0)) return;
   const int j1 = min(ntile, j0 + kSumTiles);
   // Key blocks whose partials the chunk needs: all, or (causal) those holding a key <= its last
   // query.
@@ -1813,14 +1810,11 @@ int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d) {
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQT - 1) / kQT); }
 bool bwd_needs_prep(bool split, int d) { return !split || d > 64; }
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
-  const int64_t nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT, bh = b * h;
-  if (d > 64 || nkb > kSumMaxBlocks) return 0;
-  const int64_t nchunk = (ntile + kSumTiles - 1) / kSumTiles;
-  // Causal: the key blocks of a (b, h) share an XCD when 8 divides b h.
-  if (causal) return bh % 8 == 0 ? bh * nchunk : 0;
-  // Non-causal: XCD x holds key blocks [x F, (x + 1) F) of the (b h)-major order, F = full / 8.
-  const int64_t f = ((nkb * bh) & ~int64_t{7}) / 8;
-  return f % nkb == 0 && f > 0 ? 8 * (f / nkb) * nchunk : 0;
+  // The range check keeps b h s (hence every count below) inside int32.
+  const int nkb = static_cast<int>((s + kBwdKeys - 1) / kBwdKeys);
+  const int ntile = static_cast<int>((s + kQT - 1) / kQT);
+  const SumPlan p = sum_plan(static_cast<int>(b * h), nkb, ntile, d, causal);
+  return int64_t{8} * p.per * p.nchunk;
 }
 int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal) {
   const int64_t tiles = bwd_dq_blocks(b, h, s);
@@ -1863,8 +1857,10 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   const int64_t nsum = split ? bwd_sum_blocks(b, h, s, d, causal) : 0;
   const int64_t nmain = (bwd_main_blocks(b, h, s) + 7) & ~int64_t{7};
   if (nsum == 0) arrive = nullptr, done = nullptr, epoch_slot = nullptr;
-  BwdArgs a{q,    k,     v,    d_o,  o, lse, dsum, dqkv, part, arrive, done, epoch_slot, epoch,
-            static_cast<int>(nmain), turn, ctrl, b, h, s, nkb, ntile, scale, causal, stagger};
+  const SumPlan plan = sum_plan(b * h, nkb, ntile, d, causal);
+  BwdArgs a{q,    k,     v,    d_o,  o,    lse,   dsum,       dqkv,  part,
+            arrive, done, epoch_slot, epoch, static_cast<int>(nmain), plan, turn, ctrl, b, h, s,
+            nkb,  ntile, scale, causal, stagger};
   void* args[] = {&a};
   if (split && d <= 64) {
     const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32>)

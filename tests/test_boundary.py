@@ -233,3 +233,71 @@ def test_slice_offsets_must_fit_32_bits():
     rc = L.fattn_fwd_f32_d64(BAD, BAD, BAD, BAD, BAD, 1, 1, 8, 64, 0.1, 0, ok, st, ok, None)
     assert rc == _lib.FATTN_ERANGE
     assert "4 GiB" in _lib.last_error()
+
+
+def test_step1_grid_uses_64_bit_thread_indices():
+    """Step 1 runs b h s / 16 workgroups of 256 threads at d 64: from b h s = 2^27 rows on, a
+    32-bit thread index would wrap negative (its counter clear would write before the buffer).
+    The kernel indexes threads in 64 bits, so the range check admits such shapes: a call at
+    2^27 rows passes it and fails only at the (missing) workspace, before any launch; past the
+    int32 row limit the range check refuses."""
+    L = _lib.lib()
+    st = a3(0, 0, 64)
+    rows = 1 << 27
+    for b, h, s in ((1, 1 << 7, 1 << 20), (1 << 7, 1, 1 << 20), (1 << 10, 1 << 10, 1 << 7)):
+        assert b * h * s == rows
+        rc = L.fattn_bwd_prep_f32(BAD, BAD, st, None, 0, b, h, s, 64, None)
+        assert rc == _lib.FATTN_EWORKSPACE, _lib.last_error()
+    rc = L.fattn_bwd_prep_f32(BAD, BAD, st, None, 0, 1 << 11, 1 << 10, 1 << 10, 64, None)
+    assert rc == _lib.FATTN_ERANGE
+    assert "exceeds i32 indexing" in _lib.last_error()
+
+
+def sum_audit(b, h, s, d, causal):
+    L = _lib.lib()
+    f = L.fattn_internal_sum_audit
+    f.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.POINTER(ctypes.c_int64)]
+    f.restype = ctypes.c_int
+    out = (ctypes.c_int64 * 5)()
+    assert f(b, h, s, d, int(causal), out) == 0
+    return dict(zip(("grid", "targets", "bad", "twice", "covered"), list(out)))
+
+
+def expected_sum_bh(bh, s, causal):
+    """Restated from the schedule's definition: the (b, h)s whose key blocks all run on one XCD
+    when workgroups go to the 8 XCDs round-robin. Non-causal: (b, h)-major key blocks under
+    xcd_remap, XCD x holding items [x F, (x + 1) F), F = floor(nkb b h / 8) -- a whole number of
+    (b, h)s per XCD or no sums; causal: 8 must divide b h."""
+    nkb = -(-s // 64)
+    if nkb > 256:
+        return 0
+    if causal:
+        return bh if bh % 8 == 0 else 0
+    f = (nkb * bh) // 8
+    return 8 * (f // nkb) if f > 0 and f % nkb == 0 else 0
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_step2_dq_sum_schedule(causal):
+    """Step 2's summing workgroups, over many shapes (the kernel's own scheduling functions, run
+    on the host): every key block a summing workgroup waits for runs on that workgroup's XCD, no
+    target lies past b h (the case a rounded-up per-XCD count once produced: nkb = 1, b h not a
+    multiple of 8, e.g. h 17 s 50), no tile is summed twice, and exactly the (b, h)s the schedule's
+    definition puts wholly on one XCD are summed, every one of their tiles."""
+    n = 0
+    for s in (1, 16, 50, 64, 65, 100, 128, 200, 240, 333, 1024, 2048):
+        for bh in list(range(1, 41)) + [48, 64, 96, 192, 384]:
+            for d in (32, 64, 128):
+                a = sum_audit(1, bh, s, d, causal)
+                ntile = -(-s // 16)
+                want_bh = expected_sum_bh(bh, s, causal) if d <= 64 else 0
+                assert a["bad"] == 0 and a["twice"] == 0, (s, bh, d, a)
+                assert a["covered"] == want_bh * ntile, (s, bh, d, a, want_bh)
+                nchunk = -(-ntile // 3)
+                assert a["grid"] == want_bh * nchunk and a["targets"] == a["grid"], (s, bh, d, a)
+                n += 1
+    assert n > 1000
+    # The advisor's case: b 1, h 17, s 50 (one key block per (b, h)): 16 heads summed in step 2.
+    if not causal:
+        a = sum_audit(1, 17, 50, 64, False)
+        assert a["covered"] == 16 * 4 and a["bad"] == 0

@@ -198,3 +198,35 @@ def test_split_merge_heads(orc):
     assert q.shape == (2, 3, 5, 8)
     assert np.array_equal(orc.merge_heads(q), x[:, :, :24])
     assert np.array_equal(orc.merge_heads(v), x[:, :, 48:])
+
+
+# --- the scorer: every parity bar is an upper bound on these, so they are pinned by hand ------
+
+def test_rel_fro_hand_computed(orc):
+    """rel_fro = ||x - ref||_2 / ||ref||_2 (bench/compare.py:524-527) on cases computed by hand.
+    A scorer that under-reports (squared norms, a max in place of the 2-norm, the norm of x in the
+    denominator, an absolute instead of a relative figure) fails one of them."""
+    ref = np.zeros(5)
+    ref[0] = 3.0
+    x = ref.copy()
+    x[1] = 0.5
+    assert orc.rel_fro(x, ref) == 0.5 / 3.0
+    # ||(3, 4)|| = 5 against ||(6, 8)|| = 10, in any shape
+    ref = np.array([[6.0, 0.0], [0.0, 8.0]])
+    x = ref + np.array([[3.0, 0.0], [0.0, -4.0]])
+    assert orc.rel_fro(x, ref) == 0.5
+    assert orc.rel_fro(x.astype(np.float32), ref) == 0.5
+    # the error of a uniform relative perturbation is that perturbation
+    rng = np.random.default_rng(0)
+    ref = rng.standard_normal((4, 7, 3))
+    assert abs(orc.rel_fro(ref * (1 + 1e-3), ref) - 1e-3) < 1e-15
+    assert orc.rel_fro(ref, ref) == 0.0
+    # a zero reference: the absolute norm of the difference
+    assert orc.rel_fro(np.array([3.0, 4.0]), np.zeros(2)) == 5.0
+
+
+def test_max_abs_hand_computed(orc):
+    ref = np.array([1.0, -2.0, 3.0])
+    assert orc.max_abs(ref + np.array([0.25, -0.5, 0.125]), ref) == 0.5
+    assert orc.max_abs(np.array([-1.0, -2.0, 3.0]), ref) == 2.0
+    assert orc.max_abs(np.zeros(0), np.zeros(0)) == 0.0

@@ -125,6 +125,93 @@ def bits(t):
     return t.contiguous().view(torch.int32).cpu()
 
 
+# --- the saved row log-sum-exp L (src/lib.rs:258, kernels/fused_attn.cu:596) ----------------
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _st(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def forward_qkv_c(qkv, h, scale, causal):
+    """fattn_qkv_forward (the op level, FusedAttentionQkv::cuda_fwd): (O [b, s, h d], L [b, h, s])."""
+    b, s, thd = qkv.shape
+    out = torch.empty(b, s, thd // 3, device=qkv.device)
+    lse = torch.empty(b, h, s, device=qkv.device)
+    _lib.check(_lib.lib().fattn_qkv_forward(
+        ctypes.c_void_p(qkv.untyped_storage().data_ptr()), qkv.storage_offset(),
+        _lib.arr(qkv.shape), _lib.arr(qkv.stride()), h, scale, int(causal), _p(out), _p(lse),
+        _st(qkv)))
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def forward_bhsd_c(q, k, v, scale, causal):
+    """fattn_forward (the op level, FusedAttention::cuda_fwd) on [b, h, s, d] views:
+    (O [b, s, h, d], L [b, h, s])."""
+    b, h, s, d = q.shape
+    out = torch.empty(b, s, h, d, device=q.device)
+    lse = torch.empty(b, h, s, device=q.device)
+    args = []
+    for t in (q, k, v):
+        args += [ctypes.c_void_p(t.untyped_storage().data_ptr()), t.storage_offset(),
+                 _lib.arr(t.shape), _lib.arr(t.stride())]
+    _lib.check(_lib.lib().fattn_forward(*args, scale, int(causal), _p(out), _p(lse), _st(q)))
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def forward_kernel_c(q, k, v, scale, causal):
+    """fattn_fwd_f32_d64 (the kernel level, cuda::forward) on [b, h, s, 64] views given by their
+    first element and (batch, head, seq) strides: (O [b, s, h, d], L [b, h, s])."""
+    b, h, s, d = q.shape
+    out = torch.empty(b, s, h, d, device=q.device)
+    lse = torch.empty(b, h, s, device=q.device)
+    st = [_lib.arr(t.stride()[:3]) for t in (q, k, v)]
+    _lib.check(_lib.lib().fattn_fwd_f32_d64(_p(q), _p(k), _p(v), _p(out), _p(lse), b, h, s, d,
+                                            scale, int(causal), *st, _st(q)))
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def check_lse(lse, ref64, ref32, tag):
+    """L against the fp64 oracle's, in absolute terms (L is a log, O(1-10) here): max-abs error
+    <= 2e-6 (1 + max |L|), or 1.5 x the fp32 composed path's own max-abs error where that is
+    larger (the reference's arithmetic on the same inputs)."""
+    got = np.asarray(lse.cpu().numpy() if torch.is_tensor(lse) else lse, dtype=np.float64)
+    ref64 = np.asarray(ref64, dtype=np.float64)
+    err = float(np.max(np.abs(got - ref64))) if got.size else 0.0
+    floor = float(np.max(np.abs(np.asarray(ref32, np.float64) - ref64))) if got.size else 0.0
+    bar = max(2e-6 * (1.0 + float(np.max(np.abs(ref64), initial=0.0))), 1.5 * floor)
+    say(f"  {tag}: L max-abs {err:.2e} (fp32 composed {floor:.2e}, bar {bar:.2e})")
+    assert got.shape == ref64.shape
+    assert np.all(np.isfinite(got)), f"{tag}: L not finite"
+    assert err <= bar, f"{tag}: L max-abs error {err:.3e} > {bar:.3e}"
+    return err
+
+
+def check_lse_all_levels(orc, qkv, h, d, scale, causal, tag, o_autograd=None):
+    """L from the three forward entries (qkv op, general op on the head views, kernel level on
+    the head views) against the oracle; their O and L are bit-identical to each other (and O to
+    the autograd op's, when given)."""
+    x = qkv.cpu().numpy()
+    _, l64 = orc.qkv_forward(x, h, scale, causal, dtype=np.float64)
+    _, l32 = orc.qkv_forward(x, h, scale, causal, dtype=np.float32)
+    o1, l1 = forward_qkv_c(qkv, h, scale, causal)
+    q, k, v = qkv_views(qkv, h, d)
+    o2, l2 = forward_bhsd_c(q, k, v, scale, causal)
+    o3, l3 = forward_kernel_c(q, k, v, scale, causal)
+    check_lse(l1, l64, l32, f"{tag} qkv op")
+    assert torch.equal(bits(l1), bits(l2)) and torch.equal(bits(l1), bits(l3)), f"{tag}: L"
+    assert torch.equal(bits(o1), bits(o2.reshape(o1.shape)))
+    assert torch.equal(bits(o1), bits(o3.reshape(o1.shape)))
+    if o_autograd is not None:
+        assert torch.equal(bits(o1), bits(o_autograd))
+    return l1
+
+
 # --- tests/parity.rs, on the GPU ------------------------------------------------------------
 
 PARITY_SHAPES = [(2, 7, 3, 64), (2, 240, 6, 64), (1, 97, 2, 64), (1, 33, 2, 64)]
@@ -147,6 +234,7 @@ def test_matches_oracle_closed_form(orc, cuda, shape, causal):
         eg = orc.max_abs(grad.cpu().numpy(), ref_grad)
         say(f"  {path}: max-abs vs fp64: out {eo:.2e} grad {eg:.2e}")
         assert max(eo, eg) <= max(BAND, 1.5 * cmax)
+    check_lse_all_levels(orc, qkv, h, d, 1.0 / d ** 0.5, causal, "closed form", out)
 
 
 def test_golden_vectors_gpu(orc, cuda):
@@ -366,6 +454,13 @@ def test_config1_general_path(orc, cuda):
         e = orc.rel_fro(a.detach().cpu().numpy(), r)
         say(f"  config1 {name} {e:.2e}")
         assert e <= REL_TOL
+    _, l32 = orc.forward(q.numpy(), k.numpy(), v.numpy(), 0.125, False, dtype=np.float32)
+    qd, kd, vd = (t.to(cuda) for t in (q, k, v))
+    o_op, l_op = forward_bhsd_c(qd, kd, vd, 0.125, False)
+    o_k, l_k = forward_kernel_c(qd, kd, vd, 0.125, False)
+    check_lse(l_op, l64, l32, "config1 general op")
+    assert torch.equal(bits(l_op), bits(l_k)) and torch.equal(bits(o_op), bits(o_k))
+    assert torch.equal(bits(o_op.transpose(1, 2)), bits(o.detach()))
 
 
 def seeded_qkv(orc, b, h, s, seed, cuda):
@@ -379,7 +474,18 @@ def test_config2_target(orc, cuda):
     x, dout, qkv, g = seeded_qkv(orc, 64, 6, 240, 0, cuda)
     ref_out, _, ref_grad = oracle_qkv(orc, x, dout, 6, 64, False, np.float64, 0.125)
     out, grad = run("fused_qkv", qkv, g, 6, 64, False, 0.125)
-    check_errors(orc, out, grad, ref_out, ref_grad, "config2")
+    errs = check_errors(orc, out, grad, ref_out, ref_grad, "config2")
+    check_lse_all_levels(orc, qkv, 6, 64, 0.125, False, "config2", out)
+    # The scorer reports a deliberate perturbation of the HIP output at its size: a relative
+    # 1e-4 random perturbation and a uniform 1e-5 rescale, each within the output's own error.
+    o = out.cpu().numpy().astype(np.float64)
+    rng = np.random.default_rng(2)
+    n = rng.standard_normal(o.shape)
+    delta = n * (1e-4 * np.linalg.norm(ref_out) / np.linalg.norm(n))
+    for name, pert, size in (("random", o + delta, 1e-4), ("rescale", o * (1 + 1e-5), 1e-5)):
+        got = orc.rel_fro(pert, ref_out)
+        say(f"  perturbed output ({name} {size:.0e}): scored {got:.4e}")
+        assert abs(got - size) <= 2 * errs["o"] + 1e-3 * size, (name, got)
 
 
 def test_config3_causal_reruns(orc, cuda, dq_sum):
@@ -389,6 +495,8 @@ def test_config3_causal_reruns(orc, cuda, dq_sum):
     ref_out, _, ref_grad = oracle_qkv(orc, x, dout, 6, 64, True, np.float64, 0.125)
     out, grad = run("fused_qkv", qkv, g, 6, 64, True, 0.125)
     check_errors(orc, out, grad, ref_out, ref_grad, "config3")
+    if dq_sum == "split":
+        check_lse_all_levels(orc, qkv, 6, 64, 0.125, True, "config3", out)
     first = bits(grad)
     for rerun in range(10):
         _, g2 = run("fused_qkv", qkv, g, 6, 64, True, 0.125)
@@ -407,15 +515,22 @@ def sample_slices(n_b, n_h, count, seed):
     return sorted((int(p) // n_h, int(p) % n_h) for p in picks)
 
 
-def check_sampled(orc, q, k, v, do, o, dq, dk, dv, scale, causal, slices, tag):
-    """fp64 oracle on a seeded sample of (b, h) slices; the full tensors on invariants."""
+def check_sampled(orc, q, k, v, do, o, dq, dk, dv, scale, causal, slices, tag, lse=None):
+    """fp64 oracle on a seeded sample of (b, h) slices (O, dQ, dK, dV, and L when given); the full
+    tensors on invariants."""
     sl = lambda t, b, h: np.asarray(t[b:b + 1, h:h + 1], dtype=np.float64)  # noqa: E731
     errs = {"o": [], "dq": [], "dk": [], "dv": []}
     num = {k_: 0.0 for k_ in errs}
     den = {k_: 0.0 for k_ in errs}
+    l_got, l_ref, l_32 = [], [], []
     for (b, h) in slices:
         qs, ks, vs, ds = sl(q, b, h), sl(k, b, h), sl(v, b, h), sl(do, b, h)
         o64, l64 = orc.forward(qs, ks, vs, scale, causal, dtype=np.float64)
+        if lse is not None:
+            _, l32 = orc.forward(qs, ks, vs, scale, causal, dtype=np.float32)
+            l_got.append(np.asarray(lse[b:b + 1, h:h + 1], np.float64))
+            l_ref.append(l64)
+            l_32.append(l32)
         dq64, dk64, dv64 = orc.backward(qs, ks, vs, o64, l64, ds, scale, causal,
                                         dtype=np.float64)
         for name, got, ref in (("o", o, o64), ("dq", dq, dq64), ("dk", dk, dk64),
@@ -428,6 +543,9 @@ def check_sampled(orc, q, k, v, do, o, dq, dk, dv, scale, causal, slices, tag):
         " ".join(f"{k_} {v_:.2e}" for k_, v_ in rel.items()))
     for k_, v_ in rel.items():
         assert v_ <= REL_TOL, f"{tag}: {k_} {v_:.3e}"
+    if lse is not None:
+        check_lse(np.concatenate(l_got), np.concatenate(l_ref), np.concatenate(l_32),
+                  f"{tag} (sampled)")
     # Invariants over every slice: sum_j dK_j = 0, sum_j dV_j = sum_i dO_i.
     dk_sum = np.abs(np.asarray(dk, np.float64).sum(axis=2)).max()
     dv_err = np.abs(np.asarray(dv, np.float64).sum(axis=2)
@@ -445,11 +563,13 @@ def test_config4_long_causal(orc, cuda):
     x, dout, qkv, g = seeded_qkv(orc, b, h, s, 2, cuda)
     say("config4 run")
     out, grad = run("fused_qkv", qkv, g, h, d, True, 0.125)
+    o_c, lse = forward_qkv_c(qkv, h, 0.125, True)
+    assert torch.equal(bits(o_c), bits(out))
     q, k, v = orc.split_heads(x, h)
     do, o = to_heads(dout, h), to_heads(out.cpu().numpy(), h)
     dq, dk, dv = orc.split_heads(grad.cpu().numpy(), h)
     check_sampled(orc, q, k, v, do, o, dq, dk, dv, 0.125, True, sample_slices(b, h, 6, 4),
-                  "config4")
+                  "config4", lse=lse.cpu().numpy())
 
 
 def test_config5_strided_views_large_logits(orc, cuda):
@@ -467,10 +587,14 @@ def test_config5_strided_views_large_logits(orc, cuda):
     o = cfa.fused_attention(q, k, v, 0.125, False)
     o.backward(do.to(cuda))
     torch.cuda.synchronize()
+    o_op, lse = forward_bhsd_c(qg, kg, vg, 0.125, False)
+    o_k, lse_k = forward_kernel_c(qg, kg, vg, 0.125, False)
+    assert torch.equal(bits(lse), bits(lse_k)) and torch.equal(bits(o_op), bits(o_k))
+    assert torch.equal(bits(o_op.transpose(1, 2)), bits(o.detach()))
     qn, kn, vn = (t.transpose(1, 2).numpy() for t in bufs)
     dq, dk, dv = (t.grad.transpose(1, 2).cpu().numpy() for t in leaves)
     check_sampled(orc, qn, kn, vn, do.numpy(), o.detach().cpu().numpy(), dq, dk, dv, 0.125,
-                  False, sample_slices(16, 16, 6, 5), "config5")
+                  False, sample_slices(16, 16, 6, 5), "config5", lse=lse.cpu().numpy())
 
 
 @pytest.mark.parametrize("s", [4096, 4160])
@@ -702,3 +826,10 @@ def test_scale_signs(orc, cuda, causal):
         out, grad = run("fused_qkv", qkv, wt, h, d, causal, scale)
         floor, _ = composed_floor(orc, x, w, h, d, causal, ref_out, ref_grad, scale)
         check_errors(orc, out, grad, ref_out, ref_grad, f"scale {scale}", floor)
+        lse = check_lse_all_levels(orc, qkv, h, d, scale, causal, f"scale {scale}", out)
+        if scale == 0.0:
+            # uniform attention: L_i = ln(number of keys query i sees)
+            n = np.arange(1, s + 1) if causal else np.full(s, s)
+            want = np.broadcast_to(np.log(n.astype(np.float64)), (b, h, s))
+            got = lse.cpu().numpy().astype(np.float64)
+            assert np.max(np.abs(got - want)) <= 4e-7 * np.log(s), "L = ln n at scale 0"
