@@ -29,6 +29,7 @@ EXPORTS = (
     "fattn_bwd_main_f32",
     "fattn_bwd_dq_f32",
     "fattn_bwd_f32",
+    "fattn_bwd_f32_noalloc",
     "fattn_fwd_f32_d64",
     "fattn_bwd_prep_f32_d64",
     "fattn_bwd_main_f32_d64",
@@ -84,6 +85,8 @@ def _declare(L: ctypes.CDLL) -> None:
                                                          C_INT, P]
         getattr(L, "fattn_bwd_f32" + sfx).argtypes = [P, P, P, P, P, P, P, P, SIZE, I64, I64, I64,
                                                       I64, C_FLOAT, C_INT, A3, A3, A3, A3, P]
+    L.fattn_bwd_f32_noalloc.argtypes = [P, P, P, P, P, P, P, I64, I64, I64, I64, C_FLOAT, C_INT,
+                                        A3, A3, A3, A3, P]
     L.fattn_qkv_forward.argtypes = [P, I64, A3, A3, I64, C_FLOAT, C_INT, P, P, P]
     L.fattn_qkv_backward.argtypes = [P, I64, A3, A3, I64, C_FLOAT, C_INT, P, P, P, I64, A3, A3,
                                      P, P, SIZE, P]

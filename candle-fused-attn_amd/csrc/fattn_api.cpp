@@ -421,6 +421,37 @@ int fattn_bwd_f32(const float* q, const float* k, const float* v, const float* o
                       workspace, workspace_bytes, b, h, s, d, scale, causal, stream);
 }
 
+int fattn_bwd_f32_noalloc(const float* q, const float* k, const float* v, const float* o,
+                          const float* d_o, const float* lse, float* dqkv, int64_t b, int64_t h,
+                          int64_t s, int64_t d, float scale, int causal,
+                          const int64_t q_strides[3], const int64_t k_strides[3],
+                          const int64_t v_strides[3], const int64_t do_strides[3], void* stream) {
+  const char* who = "fused_attention";
+  if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
+  if (int rc = check_head_dim(d)) return rc;
+  if (empty3(b, h, s)) return ok();
+  if (!q_strides || !k_strides || !v_strides || !do_strides) {
+    return fail(FATTN_EINVAL, "fused_attention: null strides");
+  }
+  if (int rc = check_range(who, b, h, s, d)) return rc;
+  // The split sum when its workspace fits in the scratch, else the turn hand-over.
+  const fattn::Workspace l = fattn::workspace_layout(b, h, s, d);
+  const size_t need = l.bytes_split <= FATTN_STATIC_SCRATCH_BYTES ? l.bytes_split : l.bytes_min;
+  if (need > FATTN_STATIC_SCRATCH_BYTES) {
+    return fail(FATTN_EWORKSPACE,
+                std::string(who) + ": the backward of " + std::to_string(b) + " x " +
+                    std::to_string(h) + " x " + std::to_string(s) + " needs a workspace of " +
+                    std::to_string(need) + " bytes; the static scratch holds " +
+                    std::to_string(FATTN_STATIC_SCRATCH_BYTES) +
+                    " (pass a workspace to fattn_bwd_f32)");
+  }
+  void* ws = nullptr;
+  if (int err = fattn::static_scratch(stream, &ws)) return hip_fail(err, "static scratch");
+  return run_backward(who, make_view(q, q_strides), make_view(k, k_strides),
+                      make_view(v, v_strides), o, make_view(d_o, do_strides), lse, dqkv, ws, need,
+                      b, h, s, d, scale, causal, stream);
+}
+
 // The reference-named head_dim-64 entries: the generic ones behind the reference's check.
 int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,
                       int64_t b, int64_t h, int64_t s, int64_t d, float scale, int causal,

@@ -128,6 +128,10 @@ int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long lon
                   const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
                   float scale, int causal, void* stream);
 
+// The device address of the library's static scratch (FATTN_STATIC_SCRATCH_BYTES, the workspace
+// of fattn_bwd_f32_noalloc) on the device that runs `stream`; a hipError_t value as int.
+int static_scratch(void* stream, void** out);
+
 // Grid sizes the launchers will use (for range checks before launching).
 int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal, int d);
 int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s);

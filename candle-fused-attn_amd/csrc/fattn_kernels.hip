@@ -34,10 +34,19 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <stddef.h>
 #include <stdint.h>
 
+#include "fattn.h"
 #include "fattn_internal.h"
+
+// The backward workspace of fattn_bwd_f32_noalloc, for callers that cannot allocate: device memory
+// of this library, one copy per GPU (each at its own address), held until the process ends. In
+// host code the name is only a host-side handle: the device address comes from
+// hipGetSymbolAddress (fattn::static_scratch below), never from the name itself.
+static __device__ __align__(256) unsigned char scratch[FATTN_STATIC_SCRATCH_BYTES];
 
 namespace fattn {
 namespace {
@@ -1879,6 +1888,39 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
     fn = reinterpret_cast<const void*>(bwd_kernel<false, 64>);
   }
   return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
+}
+
+// The device address of `scratch` on the device that runs `stream` (the null stream: the current
+// device), looked up with hipGetSymbolAddress once per device, with that device current, and kept.
+int static_scratch(void* stream, void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> addr[kMaxDevices];
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev)
+                        : hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return static_cast<int>(hipErrorInvalidDevice);
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(mu);
+    p = addr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      int cur = 0;
+      if ((e = hipGetDevice(&cur)) != hipSuccess) return static_cast<int>(e);
+      if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return static_cast<int>(e);
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (cur != dev) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+      }
+      if (e != hipSuccess) return static_cast<int>(e);
+      if (p == nullptr) return static_cast<int>(hipErrorInvalidSymbol);
+      addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
 }
 
 int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long long* arrive,

@@ -123,6 +123,22 @@ int fattn_bwd_f32(const float* q, const float* k, const float* v, const float* o
                   const int64_t k_strides[3], const int64_t v_strides[3],
                   const int64_t do_strides[3], void* stream);
 
+/* fattn_bwd_f32 without the workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no
+ * counterpart in the reference. It calls no allocating routine: the workspace is the library's
+ * static scratch, FATTN_STATIC_SCRATCH_BYTES of device memory per GPU, held until the process
+ * ends. dQ is summed the split way when that workspace fits in the scratch, else by turns (the
+ * same kernels and results as fattn_bwd_f32 with a workspace of that size); a shape whose minimum
+ * workspace exceeds the scratch is refused with FATTN_EWORKSPACE before any launch. Every call on
+ * one GPU shares that GPU's scratch: calls that overlap on one GPU (two streams, two threads)
+ * race and must be ordered by the caller. */
+#define FATTN_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+int fattn_bwd_f32_noalloc(const float* q, const float* k, const float* v, const float* o,
+                          const float* d_o, const float* lse, float* dqkv, int64_t b, int64_t h,
+                          int64_t s, int64_t d, float scale, int causal,
+                          const int64_t q_strides[3], const int64_t k_strides[3],
+                          const int64_t v_strides[3], const int64_t do_strides[3], void* stream);
+
 /* The same five under the reference's kernel names, with its head_dim check (d must be 64,
  * else FATTN_EHEADDIM with the reference's message, src/cuda.rs:85-93). */
 int fattn_fwd_f32_d64(const float* q, const float* k, const float* v, float* o, float* lse,

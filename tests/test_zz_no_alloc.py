@@ -1,0 +1,86 @@
+"""fattn_bwd_f32_noalloc (the backward with the library's static scratch as its workspace) against
+fattn_bwd_f32 with a caller's workspace of the kind the no-alloc entry picks (split when the split
+workspace fits in FATTN_STATIC_SCRATCH_BYTES, else turns): bit-identical dQ, dK, dV on two calls
+in a row, the second on a smaller shape, causal and not, and the refusal of a shape whose minimum
+workspace exceeds the scratch (before any launch)."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from candle_fused_attn import _lib
+
+pytestmark = pytest.mark.gpu
+
+STATIC_SCRATCH = 64 << 20  # FATTN_STATIC_SCRATCH_BYTES (include/fattn.h)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def P(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def backward_both(b, h, s, d, causal, seed, dev):
+    """(dqkv from fattn_bwd_f32_noalloc, dqkv from fattn_bwd_f32 with a workspace of the same
+    kind, the kind) for seeded N(0, 1) qkv and output gradient."""
+    L = _lib.lib()
+    rng = np.random.default_rng(seed)
+    qkv = torch.from_numpy(rng.standard_normal((b, s, 3 * h * d)).astype(np.float32)).to(dev)
+    dout = torch.from_numpy(rng.standard_normal((b, s, h * d)).astype(np.float32)).to(dev)
+    st = _lib.arr([s * 3 * h * d, d, 3 * h * d])
+    gst = _lib.arr([s * h * d, d, h * d])
+    qp, kp, vp = (ctypes.c_void_p(qkv.data_ptr() + i * h * d * 4) for i in range(3))
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    scale = 1.0 / d ** 0.5
+    o = torch.empty(b, s, h * d, device=dev)
+    lse = torch.empty(b, h, s, device=dev)
+    _lib.check(L.fattn_fwd_f32(qp, kp, vp, P(o), P(lse), b, h, s, d, scale, int(causal), st, st,
+                               st, stream))
+    split = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
+    n = split if split <= STATIC_SCRATCH else L.fattn_bwd_workspace_min_bytes(b, h, s, d)
+    kind = "split" if n == split else "turns"
+    ws = torch.empty(n, dtype=torch.uint8, device=dev)
+    want = torch.full_like(qkv, float("nan"))
+    _lib.check(L.fattn_bwd_f32(qp, kp, vp, P(o), P(dout), P(lse), P(want), P(ws), n, b, h, s, d,
+                               scale, int(causal), st, st, st, gst, stream))
+    got = torch.full_like(qkv, float("nan"))
+    _lib.check(L.fattn_bwd_f32_noalloc(qp, kp, vp, P(o), P(dout), P(lse), P(got), b, h, s, d,
+                                       scale, int(causal), st, st, st, gst, stream))
+    torch.cuda.synchronize()
+    return got, want, kind
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_noalloc_matches_workspace_entry(cuda, causal):
+    # (b, h, s, d): split fits the scratch, then a smaller split shape; the config-2 shape (its
+    # split workspace exceeds the scratch: turns), then a smaller one; head_dim 32 and 128.
+    cases = [((4, 6, 240, 64), (2, 3, 97, 64)),
+             ((64, 6, 240, 64), (8, 6, 200, 64)),
+             ((2, 4, 333, 32), (1, 2, 65, 32)),
+             ((2, 3, 150, 128), (1, 1, 17, 128))]
+    for big, small in cases:
+        for i, (b, h, s, d) in enumerate((big, small)):
+            say(f"noalloc b{b} h{h} s{s} d{d} causal={causal} call {i + 1}")
+            got, want, kind = backward_both(b, h, s, d, causal, seed=b * 1000 + s, dev=cuda)
+            assert torch.isfinite(want).all()
+            assert torch.equal(got.view(torch.int32), want.view(torch.int32)), (b, h, s, d, kind)
+            say(f"  {kind}: bit-identical")
+
+
+def test_noalloc_refuses_what_does_not_fit(cuda):
+    """A minimum workspace above the scratch is refused up front (FATTN_EWORKSPACE, no launch)."""
+    L = _lib.lib()
+    b, h, s, d = 1, 64, 1 << 18, 64   # D alone: 2^24 rows x 4 bytes = 64 MiB, plus counters
+    assert L.fattn_bwd_workspace_min_bytes(b, h, s, d) > STATIC_SCRATCH
+    st = _lib.arr([0, 0, 64])
+    bad = ctypes.c_void_p(0x1000)
+    rc = L.fattn_bwd_f32_noalloc(bad, bad, bad, bad, bad, bad, bad, b, h, s, d, 0.125, 0, st, st,
+                                 st, st, None)
+    assert rc == _lib.FATTN_EWORKSPACE
+    assert "static scratch" in _lib.last_error()
