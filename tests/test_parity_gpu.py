@@ -668,6 +668,69 @@ def test_dq_sums_in_step2_match_step3(orc, cuda, d, h, s):
                                       False, np.float64, 0.125)
     check_errors(orc, o[:, :, 0].contiguous(), g[:, :, :, 0].reshape(1, s, 3 * d), ref_out,
                  ref_grad, "head 0")
+    # Which tiles step 2 summed: after step 2 alone, the done flags that hold the launch's epoch
+    # (recorded in the workspace) are exactly the tiles of the (b, h)s the schedule gives the
+    # summing workgroups; step 3 then sums the rest, and the gradient is the op level's.
+    summed = step2_summed_tiles(torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), h, d,
+                                False, grad)
+    from test_boundary import expected_sum_bh
+    n_bh = expected_sum_bh(h, s, False)
+    ntile = -(-s // 16)
+    want = np.zeros((h, ntile), dtype=bool)
+    want[:n_bh] = True
+    say(f"  step 2 summed {int(summed.sum())} of {summed.size} tiles (schedule: {n_bh} heads)")
+    assert np.array_equal(summed, want)
+
+
+def ws_layout(b, h, s, d):
+    """Byte offsets of the backward workspace's parts (restated from fattn_api.cpp's
+    workspace_layout; the library's reported sizes pin it)."""
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    tiles, nkb = b * h * (-(-s // 16)), -(-s // 64)
+    lay = {"d": 0, "turn": up(b * h * s * 4)}
+    lay["ctrl"] = lay["turn"] + up(tiles * 4)
+    lay["part"] = lay["ctrl"] + 256
+    lay["arrive"] = lay["part"] + up(nkb * tiles * 16 * d * 4)
+    lay["done"] = lay["arrive"] + up(b * h * nkb * 8)
+    lay["epoch"] = lay["done"] + up(tiles * 8)
+    L = _lib.lib()
+    assert L.fattn_bwd_workspace_min_bytes(b, h, s, d) == lay["part"]
+    assert L.fattn_bwd_workspace_split_bytes(b, h, s, d) == lay["epoch"] + 256
+    return lay
+
+
+def step2_summed_tiles(qkv, dout, h, d, causal, grad_want):
+    """Runs the split backward kernel by kernel on the qkv views; returns the [b h, ntile] mask of
+    the query tiles step 2 summed itself (done flag == the launch's epoch, read before step 3
+    clears them), and checks that the three steps give `grad_want` bit for bit."""
+    b, s, _ = qkv.shape
+    L = _lib.lib()
+    P = _p
+    st = _lib.arr([s * 3 * h * d, d, 3 * h * d])
+    gst = _lib.arr([s * h * d, d, h * d])
+    qp, kp, vp = (ctypes.c_void_p(qkv.data_ptr() + i * h * d * 4) for i in range(3))
+    stream = _st(qkv)
+    o = torch.empty(b, s, h * d, device=qkv.device)
+    lse = torch.empty(b, h, s, device=qkv.device)
+    _lib.check(L.fattn_fwd_f32(qp, kp, vp, P(o), P(lse), b, h, s, d, 0.125, int(causal), st, st,
+                               st, stream))
+    lay = ws_layout(b, h, s, d)
+    n = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
+    ws = torch.zeros(n, dtype=torch.uint8, device=qkv.device)
+    dqkv = torch.empty_like(qkv)
+    _lib.check(L.fattn_bwd_prep_f32(P(o), P(dout), gst, P(ws), n, b, h, s, d, stream))
+    _lib.check(L.fattn_bwd_main_f32(qp, kp, vp, P(o), P(dout), P(lse), P(dqkv), P(ws), n, b, h, s,
+                                    d, 0.125, int(causal), st, st, st, gst, stream))
+    torch.cuda.synchronize()
+    raw = ws.cpu().numpy()
+    ntile = -(-s // 16)
+    done = raw[lay["done"]:lay["done"] + b * h * ntile * 8].view(np.uint64).reshape(b * h, ntile)
+    epoch = raw[lay["epoch"]:lay["epoch"] + 8].view(np.uint64)[0]
+    assert epoch != 0
+    _lib.check(L.fattn_bwd_dq_f32(P(dqkv), P(ws), n, b, h, s, d, 0.125, int(causal), stream))
+    torch.cuda.synchronize()
+    assert torch.equal(bits(dqkv), bits(grad_want))
+    return done == epoch
 
 
 @pytest.mark.parametrize("d", [32, 64])
@@ -692,6 +755,9 @@ def test_causal_dq_sums_match_turns(orc, cuda, d):
     assert torch.equal(bits(o1), bits(o2)) and torch.equal(bits(g1), bits(g2))
     ref_out, _, ref_grad = oracle_qkv(orc, x, w, h, d, True, np.float64, 0.125)
     check_errors(orc, o1, g1, ref_out, ref_grad, f"causal d{d}")
+    summed = step2_summed_tiles(qkv, wt, h, d, True, g1)
+    say(f"  step 2 summed {int(summed.sum())} of {summed.size} tiles")
+    assert summed.all(), "causal, 8 | b h: step 2 sums every tile"
 
 
 @pytest.mark.parametrize("causal", [False, True])
