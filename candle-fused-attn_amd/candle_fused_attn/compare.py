@@ -1,549 +1,552 @@
-"""The fused attention against PyTorch-ROCm's fp32 attentions on MI355X: accuracy and speed,
-measured the same way for every candidate (the method of the reference's harness,
-bench/compare.py:1-38, with rocprofv3 in place of nsys and every candidate in Python).
+"""Head-to-head of the fused attention with PyTorch-ROCm's own fp32 attentions on one MI355X.
 
-Every candidate computes the same unit of work: the fused projection qkv [b, s, 3 h 64] to the
-merged output [b, s, h 64] (head split and merge included), and the backward from dout to dqkv
-through the loss head sum(o * dout):
-  fattn_qkv            fused_attention_qkv (libfattn.so)
-  fattn_general        fused_attention on the q / k / v views of qkv, output merged back
-  torch_composed       softmax((q scale) k^T) v written out in torch ops (bench/compare.py:278-289)
-  torch_sdpa_math      scaled_dot_product_attention, MATH backend forced
-  torch_sdpa_efficient scaled_dot_product_attention, EFFICIENT_ATTENTION backend forced
-The FLASH backend is probed too; a backend that refuses these inputs is recorded with its reason
-and left out of the timings.
+This is the report the reference publishes for its CUDA build against PyTorch-CUDA
+(bench/compare.py, bench/results/*-compare-v0.4.md): agreement with a float64 recompute, bit
+equality of reruns, timing in alternated rounds with a decision rule, and per-call kernel time
+from a profiler. Here every contender is Python on one device, so the design is in-process:
 
-Method (one child process per step; the parent never touches the GPU):
-  1. inputs: qkv then dout ~ N(0, 1), fp32, drawn on the CPU by torch.Generator().manual_seed(seed)
-     (bench/compare.py:496-503), saved once; every child reads them.
-  2. accuracy: each candidate's o, dq, dk, dv against an fp64 recompute on the CPU (torch autograd
-     of the composed math): max-abs and normwise relative error; the floor is the fp64 reference
-     rounded to fp32. Determinism: a second forward + backward compared bit for bit.
-  3. wall time: R rounds, the candidate order rotated each round; per candidate and phase, W warm-up
-     calls, then S samples of N back-to-back calls between two device syncs (ms per call); phases
-     fwd (no autograd), train (forward + head + backward), head (the head alone); net = train - head.
-  4. decision rule: X is faster than Y on a phase iff X's worst round median is below Y's best
-     round median (bench/compare.py:84-110); otherwise "not separated".
-  5. kernel time (--kernels): one child per candidate and phase under
-     `rocprofv3 --kernel-trace --stats`; per-call time = a kernel's total / its launches per call;
-     kernels whose launch count is not a multiple of the calls are listed as irregular.
+* Contenders. Each one maps the fused projection qkv [b, s, 3 h d] (a leaf tensor) to the merged
+  output [b, s, h d], so head split and merge are part of every timed call:
+    fattn.qkv        fused_attention_qkv (libfattn.so, hand-written gfx950 kernels)
+    fattn.views      fused_attention on the q / k / v views of qkv, output merged back
+    torch.eager      explicit softmax((q k^T) scale) v in torch ops (hipBLASLt matmuls)
+    sdpa.math        scaled_dot_product_attention with the MATH backend forced
+    sdpa.efficient   ... EFFICIENT_ATTENTION backend forced (AOTriton on ROCm)
+    sdpa.flash       ... FLASH_ATTENTION backend forced (refuses fp32: recorded, not timed)
+  The backward is out.backward(dout): the gradient arrives as given, with no loss head to time
+  or subtract.
+* Agreement. o, dq, dk, dv of every contender against float64 autograd of the same attention on
+  the CPU (einsum formulation, independent of every contender): normwise relative error
+  ||x - ref|| / ||ref|| and max-abs error; the floor row is the float64 result rounded to fp32.
+  Reruns: a second forward + backward compared bit for bit.
+* Timing. HIP events around `calls` back-to-back calls of one phase (`fwd` under no_grad, `step` =
+  forward + backward) give one sample in ms per call. A round takes `reps` samples of every
+  contender and phase in the order of one row of a cyclic Latin square over the contenders (row r
+  for round r), so every contender runs in every position equally often; the round's value is the
+  median of its samples.
+* Decision rule (paired by round): A is faster than B on a phase when A's round value is below B's
+  in every round; B faster when the reverse holds in every round; otherwise the pair is a tie at
+  this number of rounds. The ratio reported is of the medians over rounds.
+* Kernel time (--kernels): each contender and phase once more in a child process under
+  `rocprofv3 --kernel-trace`; the dispatches of the last `--kernel-calls` calls (the first
+  `--kernel-skip` of the fresh process run at ramping clocks and are dropped), summed per kernel
+  and divided by the calls, give ms per call. A kernel whose launches are not a whole number per
+  call is listed apart (allocator fills, one-off setup) and left out of the sum.
 
-Run on one MI355X, from the repository root:
-  PYTHONPATH=candle-fused-attn_amd python3 -m candle_fused_attn.compare run --out DIR [--kernels]
-Writes DIR/report.md and DIR/report.json (the inputs and the candidates' outputs, about 100 MB
-each at the default shape, go to DIR/data and are deleted at the end unless --keep-data).
+Run on one MI355X from the repository root:
+    PYTHONPATH=candle-fused-attn_amd python3 -m candle_fused_attn.compare report --out DIR
+Writes DIR/report.md and DIR/report.json.
 """
 from __future__ import annotations
 
 import argparse
-import contextlib
 import csv
+import io
 import json
-import os
 import shutil
 import statistics
 import subprocess
 import sys
+import tempfile
 import time
+from dataclasses import dataclass
 from pathlib import Path
+from typing import Callable
 
-HEAD_DIM = 64
-OURS = ("fattn_qkv", "fattn_general")
-TORCH = ("torch_composed", "torch_sdpa_math", "torch_sdpa_efficient")
-PHASES = ("fwd", "train", "net")
 PARTS = ("o", "dq", "dk", "dv")
+PHASES = ("fwd", "step")
+MINE = ("fattn.qkv", "fattn.views")
+SDPA_BACKENDS = {"sdpa.math": "MATH", "sdpa.efficient": "EFFICIENT_ATTENTION",
+                 "sdpa.flash": "FLASH_ATTENTION"}
 
 
-# --- pure helpers ------------------------------------------------------------------------------
+# --- statistics and the decision rule ---------------------------------------------------------
 
-def summarize(xs: list[float]) -> dict[str, float]:
-    """Median, quartiles (inclusive method), min and max.
+def latin_row(names, r: int) -> list:
+    """Row `r` of the cyclic Latin square over `names`: the order of round r.
 
-    >>> summarize([3.0, 1.0, 2.0, 4.0])
-    {'median': 2.5, 'q1': 1.75, 'q3': 3.25, 'min': 1.0, 'max': 4.0}
-    >>> summarize([2.0])['q1']
-    2.0
+    >>> latin_row(["x", "y", "z", "w"], 2)
+    ['z', 'w', 'x', 'y']
+    >>> [latin_row("pq", r) for r in range(3)]
+    [['p', 'q'], ['q', 'p'], ['p', 'q']]
     """
-    if len(xs) == 1:
-        return {"median": xs[0], "q1": xs[0], "q3": xs[0], "min": xs[0], "max": xs[0]}
-    q1, _, q3 = statistics.quantiles(xs, n=4, method="inclusive")
-    return {"median": statistics.median(xs), "q1": q1, "q3": q3, "min": min(xs), "max": max(xs)}
+    names = list(names)
+    k = r % len(names)
+    return names[k:] + names[:k]
 
 
-def faster(xs: list[float], ys: list[float]) -> bool:
-    """The decision rule: the worst of `xs` beats the best of `ys`.
+def round_value(samples: list[float]) -> float:
+    """A round's value: the median of its samples.
 
-    >>> faster([1.0, 1.2], [1.3, 1.5])
-    True
-    >>> faster([1.0, 1.4], [1.3, 1.5])
-    False
+    >>> round_value([5.0, 1.0, 3.0, 100.0])
+    4.0
     """
-    return max(xs) < min(ys)
+    return statistics.median(samples)
 
 
-def verdict(name_x: str, xs: list[float], name_y: str, ys: list[float]) -> str:
-    """The decision rule in words, with the ratio of medians.
+def paired_rule(a: list[float], b: list[float]) -> int:
+    """-1 if A's round value is below B's in every round (A faster), +1 if above in every round
+    (B faster), 0 otherwise (a tie at this number of rounds). Rounds are paired by index.
 
-    >>> verdict("a", [1.0], "b", [2.0])
-    'a faster (x2.00)'
-    >>> verdict("a", [2.0], "b", [1.0])
-    'b faster (x2.00)'
-    >>> verdict("a", [1.0, 2.0], "b", [1.5])
-    'not separated'
+    >>> paired_rule([0.20, 0.21, 0.19], [0.30, 0.22, 0.25])
+    -1
+    >>> paired_rule([0.40, 0.41], [0.30, 0.35])
+    1
+    >>> paired_rule([0.20, 0.26], [0.25, 0.22])
+    0
     """
-    mx, my = statistics.median(xs), statistics.median(ys)
-    if faster(xs, ys):
-        return f"{name_x} faster (x{my / mx:.2f})"
-    if faster(ys, xs):
-        return f"{name_y} faster (x{mx / my:.2f})"
-    return "not separated"
+    if len(a) != len(b) or not a:
+        raise ValueError("paired_rule: one value per round for both contenders")
+    if all(x < y for x, y in zip(a, b)):
+        return -1
+    if all(x > y for x, y in zip(a, b)):
+        return 1
+    return 0
 
 
-def rotate(xs, k: int) -> list:
-    """`xs` rotated left by `k` (round k's candidate order).
+def head_to_head(name_a: str, a: list[float], name_b: str, b: list[float]) -> str:
+    """The rule's outcome as a sentence, with the ratio of the medians over rounds.
 
-    >>> rotate(("a", "b", "c"), 1)
-    ['b', 'c', 'a']
-    >>> rotate(("a", "b"), 3)
-    ['b', 'a']
+    >>> head_to_head("fattn.qkv", [0.2, 0.21], "sdpa.math", [0.6, 0.63])
+    'fattn.qkv ahead, 3.00x'
+    >>> head_to_head("p", [0.9, 0.8], "q", [0.3, 0.35])
+    'q ahead, 2.62x'
+    >>> head_to_head("p", [0.2, 0.3], "q", [0.25, 0.26])
+    'no separation in 2 rounds'
     """
-    return [xs[(i + k) % len(xs)] for i in range(len(xs))]
+    rule = paired_rule(a, b)
+    ma, mb = statistics.median(a), statistics.median(b)
+    if rule < 0:
+        return f"{name_a} ahead, {mb / ma:.2f}x"
+    if rule > 0:
+        return f"{name_b} ahead, {ma / mb:.2f}x"
+    return f"no separation in {len(a)} rounds"
 
 
-def fmt_range(xs: list[float]) -> str:
-    """Median [min-max] in ms, or a dash.
+def spread(xs: list[float]) -> str:
+    """Median over rounds and its range, in ms.
 
-    >>> fmt_range([0.25, 0.2, 0.3])
-    '0.250 [0.200–0.300]'
-    >>> fmt_range([])
-    '—'
+    >>> spread([0.5, 0.25, 0.75])
+    '0.5000 (0.2500..0.7500)'
+    >>> spread([])
+    'n/a'
     """
     if not xs:
-        return "—"
-    return f"{statistics.median(xs):.3f} [{min(xs):.3f}–{max(xs):.3f}]"
+        return "n/a"
+    return f"{statistics.median(xs):.4f} ({min(xs):.4f}..{max(xs):.4f})"
 
 
-def kernel_rows(stats_csv: str) -> list[tuple[str, int, int]]:
-    """(name, total ns, launches) from rocprofv3's `*_kernel_stats.csv`.
+# --- profiler output ----------------------------------------------------------------------------
 
-    >>> kernel_rows('"Name","Calls","TotalDurationNs"\\n"k1",20,4000\\n"k2",3,60\\n')
-    [('k1', 4000, 20), ('k2', 60, 3)]
+def parse_kernel_trace(text: str, skip_calls: int, calls: int) -> list[tuple[str, int, float]]:
+    """(kernel name, launches, total ns) over the last `calls` of `skip_calls + calls` calls, from
+    rocprofv3's kernel_trace.csv (one row per dispatch). A kernel launched k times per call has
+    k (skip_calls + calls) dispatches: its first k skip_calls (in time order) are dropped. A
+    kernel whose count is not such a multiple is returned whole (then listed apart).
+
+    >>> t = ('"Kernel_Name","Start_Timestamp","End_Timestamp"\\n'
+    ...      '"a",0,50\\n"a",100,130\\n"a",200,220\\n"b",300,301\\n')
+    >>> parse_kernel_trace(t, 1, 2)
+    [('a', 2, 50.0), ('b', 1, 1.0)]
     """
+    runs: dict[str, list[tuple[int, int]]] = {}
+    for r in csv.DictReader(io.StringIO(text)):
+        runs.setdefault(r["Kernel_Name"], []).append((int(r["Start_Timestamp"]),
+                                                      int(r["End_Timestamp"])))
     rows = []
-    for r in csv.DictReader(stats_csv.splitlines()):
-        rows.append((r["Name"], int(float(r["TotalDurationNs"])), int(r["Calls"])))
+    for name, ds in runs.items():
+        ds.sort()
+        total = skip_calls + calls
+        if len(ds) % total == 0:
+            ds = ds[len(ds) // total * skip_calls:]
+        rows.append((name, len(ds), float(sum(e - b for b, e in ds))))
     return rows
 
 
-def per_call(rows: list[tuple[str, int, int]], calls: int) -> dict:
-    """Kernel time per call: kernels launched a multiple of `calls` times count in the total (with
-    their launches per call); the others are listed as irregular.
+def kernel_time_per_call(rows: list[tuple[str, int, float]], calls: int) -> dict:
+    """ms per call from kernels launched a multiple of `calls` times; the rest listed apart.
 
-    >>> p = per_call([("k1", 4000, 20), ("k2", 60, 3)], 10)
-    >>> p["ms"], p["irregular"], p["kernels"][0]["per_call"]
-    (0.0004, ['k2'], 2.0)
+    >>> t = kernel_time_per_call([("a", 8, 1600.0), ("b", 4, 4000.0), ("z", 3, 90.0)], 4)
+    >>> round(t["ms"], 6), t["other"], [(k["name"], k["per_call"]) for k in t["kernels"]]
+    (0.0014, ['z'], [('b', 1), ('a', 2)])
     """
-    regular, irregular, total = [], [], 0
-    for name, ns, n in rows:
-        if n % calls == 0:
-            regular.append({"name": name, "per_call": n / calls, "us_per_call": ns / calls / 1e3})
+    kept, other, total = [], [], 0.0
+    for name, n, ns in rows:
+        if n and n % calls == 0:
+            kept.append({"name": name, "per_call": n // calls, "us": ns / calls / 1e3})
             total += ns
         else:
-            irregular.append(name)
-    return {"ms": total / calls / 1e6, "kernels": regular, "irregular": irregular}
+            other.append(name)
+    kept.sort(key=lambda k: -k["us"])
+    return {"ms": total / calls / 1e6, "kernels": kept, "other": other}
 
 
-def short_name(kernel: str) -> str:
-    """A kernel's name without its argument list and return type.
+def short_kernel(name: str) -> str:
+    """A kernel's name without its return type, namespaces and argument list, for the report.
 
-    >>> short_name("void fattn::(anonymous namespace)::bwd_kernel<true>(fattn::BwdArgs)")
-    'fattn::(anonymous namespace)::bwd_kernel<true>'
+    >>> short_kernel("void fattn::(anonymous namespace)::fwd_kernel<64, 128>(FwdArgs)")
+    'fwd_kernel<64, 128>'
+    >>> short_kernel("__amd_rocclr_fillBufferAligned")
+    '__amd_rocclr_fillBufferAligned'
+    >>> short_kernel("void ew<4, at::native::Functor<float, float, float, Mul<float> > >(int)")
+    'ew<4, at::native::Functor<float, float, fl...>'
+    >>> short_kernel("Cijk_Ailk_Bljk_S_B_Bias_HA_S_SAV_UserArgs_MT240x256x16_MI16x16x1_SN_LDSB0")
+    'Cijk_Ailk_Bljk_S_B_Bias_HA_S_SAV_UserArgs_MT240x256x16'
     """
-    name = kernel[5:] if kernel.startswith("void ") else kernel
-    depth = 0
-    for i, ch in enumerate(name):
-        if ch == "<":
+    n = name.strip()
+    if n.endswith(")"):  # drop the argument list: back to the '(' matching the last ')'
+        depth = 0
+        for i in range(len(n) - 1, -1, -1):
+            depth += {")": 1, "(": -1}.get(n[i], 0)
+            if depth == 0:
+                n = n[:i]
+                break
+    depth, start = 0, 0
+    for i, ch in enumerate(n):  # after the last ':' or ' ' outside <...> and (...)
+        if ch in "<(":
             depth += 1
-        elif ch == ">":
+        elif ch in ">)":
             depth -= 1
-        elif ch == "(" and depth == 0 and not name[i:].startswith("(anonymous"):
-            return name[:i]
-    return name
+        elif ch in ": " and depth == 0:
+            start = i + 1
+    n = n[start:]
+    if n.startswith("Cijk_") and "_MT" in n:  # a Tensile GEMM: keep up to its macro tile
+        head, _, tail = n.partition("_MT")
+        return f"{head}_MT{tail.split('_')[0]}"
+    return n if len(n) <= 48 else n[:42] + "...>"
 
 
-# --- the candidates (child processes only) -----------------------------------------------------
+# --- contenders ---------------------------------------------------------------------------------
 
-def split_heads(qkv, heads: int):
-    """q, k, v [b, h, s, d] as views of the [b, s, 3 h d] projection."""
-    b, s, three_hd = qkv.shape
-    hidden = three_hd // 3
-    shape = (b, s, heads, hidden // heads)
-    q, k, v = qkv.split(hidden, dim=-1)
-    return tuple(t.view(shape).transpose(1, 2) for t in (q, k, v))
+@dataclass
+class Contender:
+    name: str
+    forward: Callable  # qkv [b, s, 3 h d] -> out [b, s, h d]
+    what: str
 
 
-def composed(qkv, heads: int, scale: float, causal: bool):
-    """softmax((q scale) k^T [+ causal mask]) v, merged back to [b, s, h d]; any float dtype."""
+def make_contenders(heads: int, scale: float, causal: bool) -> list[Contender]:
     import torch
-    b, s, three_hd = qkv.shape
-    q, k, v = split_heads(qkv, heads)
-    scores = (q * scale) @ k.transpose(-2, -1)
-    if causal:
-        mask = torch.ones(s, s, dtype=torch.bool, device=qkv.device).triu(1)
-        scores = scores.masked_fill(mask, float("-inf"))
-    return (torch.softmax(scores, dim=-1) @ v).transpose(1, 2).reshape(b, s, three_hd // 3)
+    import torch.nn.functional as F
 
-
-def sdpa(qkv, heads: int, scale: float, causal: bool):
-    import torch
-    b, s, three_hd = qkv.shape
-    q, k, v = split_heads(qkv, heads)
-    o = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=scale)
-    return o.transpose(1, 2).reshape(b, s, three_hd // 3)
-
-
-def fattn_general(qkv, heads: int, scale: float, causal: bool):
     import candle_fused_attn as cfa
-    b, s, three_hd = qkv.shape
-    q, k, v = split_heads(qkv, heads)
-    return cfa.fused_attention(q, k, v, scale, causal).transpose(1, 2).reshape(b, s, three_hd // 3)
 
+    def views(qkv):
+        b, s, three_hd = qkv.shape
+        d = three_hd // 3 // heads
+        return qkv.view(b, s, 3, heads, d).permute(2, 0, 3, 1, 4).unbind(0)  # [b, h, s, d] each
 
-def fattn_qkv(qkv, heads: int, scale: float, causal: bool):
-    import candle_fused_attn as cfa
-    return cfa.fused_attention_qkv(qkv, heads, scale, causal)
+    def merge(o):
+        b, h, s, d = o.shape
+        return o.transpose(1, 2).reshape(b, s, h * d)
 
+    def fattn_views(qkv):
+        q, k, v = views(qkv)
+        return merge(cfa.fused_attention(q, k, v, scale, causal))
 
-def backend_context(name: str):
-    """The forced SDPA backend of candidate `name` (none for the others)."""
-    from torch.nn.attention import SDPBackend, sdpa_kernel
-    forced = {"torch_sdpa_math": SDPBackend.MATH,
-              "torch_sdpa_efficient": SDPBackend.EFFICIENT_ATTENTION,
-              "torch_sdpa_flash": SDPBackend.FLASH_ATTENTION}
-    return sdpa_kernel([forced[name]]) if name in forced else contextlib.nullcontext()
+    def eager(qkv):
+        q, k, v = views(qkv)
+        w = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
+        if causal:
+            s = q.shape[2]
+            w = w.masked_fill(torch.ones(s, s, dtype=torch.bool, device=w.device).triu(1),
+                              float("-inf"))
+        return merge(torch.matmul(torch.softmax(w, dim=-1), v))
 
+    def sdpa_with(backend_name):
+        backend = getattr(torch.nn.attention.SDPBackend, backend_name)
 
-ATTEND = {"fattn_qkv": fattn_qkv, "fattn_general": fattn_general, "torch_composed": composed,
-          "torch_sdpa_math": sdpa, "torch_sdpa_efficient": sdpa, "torch_sdpa_flash": sdpa}
+        def run(qkv):
+            q, k, v = views(qkv)
+            with torch.nn.attention.sdpa_kernel([backend]):
+                return merge(F.scaled_dot_product_attention(q, k, v, is_causal=causal,
+                                                            scale=scale))
+        return run
 
-
-class Bench:
-    """One candidate set on the saved inputs, in a child process."""
-
-    def __init__(self, inputs: Path, heads: int, causal: bool) -> None:
-        import torch
-        from safetensors.torch import load_file
-        t = load_file(str(inputs))
-        self.qkv = t["qkv"].to("cuda").requires_grad_(True)
-        self.dout = t["dout"].to("cuda")
-        self.heads, self.causal = heads, causal
-        self.scale = 1.0 / HEAD_DIM ** 0.5
-        self.standin = torch.zeros_like(self.dout, requires_grad=True)
-
-    def attend(self, name: str, qkv):
-        return ATTEND[name](qkv, self.heads, self.scale, self.causal)
-
-    def train(self, name: str):
-        self.qkv.grad = None
-        o = self.attend(name, self.qkv)
-        (o * self.dout).sum().backward()
-        return o, self.qkv.grad
-
-    def call(self, name: str, phase: str) -> None:
-        import torch
-        if phase == "fwd":
-            with torch.no_grad():
-                self.attend(name, self.qkv)
-        elif phase == "train":
-            self.train(name)
-        else:  # the head alone
-            self.standin.grad = None
-            (self.standin * self.dout).sum().backward()
-
-
-def probe(bench: Bench, names) -> dict[str, str]:
-    """Each candidate's forward + backward once: "ok", or the error that refused it."""
-    import torch
-    out = {}
-    for name in names:
-        try:
-            with backend_context(name):
-                bench.train(name)
-            torch.cuda.synchronize()
-            out[name] = "ok"
-        except RuntimeError as e:
-            out[name] = "refused: " + " ".join(str(e).split())[:300]
+    out = [Contender("fattn.qkv", lambda x: cfa.fused_attention_qkv(x, heads, scale, causal),
+                     "fused_attention_qkv (libfattn.so)"),
+           Contender("fattn.views", fattn_views, "fused_attention on the q/k/v views"),
+           Contender("torch.eager", eager, "softmax((q k^T) scale) v in torch ops")]
+    for name, backend in SDPA_BACKENDS.items():
+        out.append(Contender(name, sdpa_with(backend), f"scaled_dot_product_attention, {backend}"))
     return out
 
 
-def side_accuracy(a) -> None:
+def reference64(qkv, dout, heads: int, scale: float, causal: bool) -> dict:
+    """o, dq, dk, dv in float64 on the CPU (autograd of an einsum formulation)."""
     import torch
-    from safetensors.torch import save_file
-    torch.set_float32_matmul_precision("highest")
-    bench = Bench(a.inputs, a.heads, a.causal)
-    status = probe(bench, OURS + TORCH + ("torch_sdpa_flash",))
-    rows = []
-    for name in OURS + TORCH:
-        if status[name] != "ok":
-            continue
-        with backend_context(name):
-            o1, g1 = bench.train(name)
-            o1, g1 = o1.detach().clone(), g1.clone()
-            o2, g2 = bench.train(name)
-        det = bool(torch.equal(o1, o2) and torch.equal(g1, g2))
-        save_file({"o": o1.contiguous().cpu(), "dqkv": g1.contiguous().cpu()},
-                  str(a.inputs.parent / f"{name}.safetensors"))
-        rows.append({"name": name, "deterministic": det})
-    env = {"torch": torch.__version__, "hip": torch.version.hip,
-           "gpu": torch.cuda.get_device_name(0),
-           "arch": getattr(torch.cuda.get_device_properties(0), "gcnArchName", "?"),
-           "cus": torch.cuda.get_device_properties(0).multi_processor_count,
-           "fp32_matmul_precision": torch.get_float32_matmul_precision()}
-    import candle_fused_attn as cfa
-    env["libfattn"] = cfa.version()
-    (a.out / "accuracy.json").write_text(json.dumps(
-        {"candidates": rows, "status": status, "env": env}, indent=1), encoding="utf-8")
+    x = qkv.detach().to("cpu", torch.float64).requires_grad_(True)
+    b, s, three_hd = x.shape
+    d = three_hd // 3 // heads
+    q, k, v = x.view(b, s, 3, heads, d).unbind(2)                      # [b, s, h, d]
+    logits = torch.einsum("bihc,bjhc->bhij", q, k) * scale
+    if causal:
+        logits = logits.masked_fill(torch.ones(s, s, dtype=torch.bool).triu(1), float("-inf"))
+    o = torch.einsum("bhij,bjhc->bihc", torch.softmax(logits, dim=-1), v).reshape(b, s, heads * d)
+    o.backward(dout.detach().to("cpu", torch.float64))
+    dq, dk, dv = x.grad.view(b, s, 3, heads * d).unbind(2)
+    return {"o": o.detach(), "dq": dq, "dk": dk, "dv": dv}
 
 
-def side_time(a) -> None:
-    import torch
-    torch.set_float32_matmul_precision("highest")
-    bench = Bench(a.inputs, a.heads, a.causal)
-    names = json.loads(a.names)
-    rows = []
-
-    def timed(name: str, phase: str) -> None:
-        for _ in range(a.warmup):
-            bench.call(name, phase)
-        ms = []
-        for _ in range(a.samples):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(a.calls):
-                bench.call(name, phase)
-            torch.cuda.synchronize()
-            ms.append((time.perf_counter() - t0) * 1e3 / a.calls)
-        rows.append({"name": name, "phase": phase, "ms": ms})
-
-    for name in rotate(names, a.round):
-        with backend_context(name):
-            timed(name, "fwd")
-            timed(name, "train")
-    timed("head", "head")
-    (a.out / f"time_r{a.round}.json").write_text(json.dumps(rows), encoding="utf-8")
+def agreement(got: dict, ref: dict) -> dict:
+    """Per part: normwise relative error and max-abs error against `ref` (float64)."""
+    res = {}
+    for p in PARTS:
+        r = ref[p]
+        diff = got[p].to("cpu").double() - r
+        den = float(r.norm())
+        res[p] = {"rel": float(diff.norm()) / den if den else float(diff.norm()),
+                  "max_abs": float(diff.abs().max()) if diff.numel() else 0.0}
+    return res
 
 
-def side_kernels(a) -> None:
-    import torch
-    torch.set_float32_matmul_precision("highest")
-    bench = Bench(a.inputs, a.heads, a.causal)
-    with backend_context(a.only):
-        for _ in range(a.calls):
-            bench.call(a.only, a.phase)
-        torch.cuda.synchronize()
+def one_step(c: Contender, qkv, dout):
+    """Forward + backward of a contender on a fresh leaf: (out, dq, dk, dv)."""
+    x = qkv.detach().clone().requires_grad_(True)
+    out = c.forward(x)
+    out.backward(dout)
+    hd = x.shape[-1] // 3
+    return out.detach(), x.grad[..., :hd], x.grad[..., hd:2 * hd], x.grad[..., 2 * hd:]
 
 
-# --- the orchestration (parent; no GPU use) ----------------------------------------------------
+# --- measurement --------------------------------------------------------------------------------
 
-def log(msg: str) -> None:
-    print(f"[{time.strftime('%H:%M:%S')}] {msg}", flush=True)
+def phase_fn(torch, c: Contender, qkv, dout, phase: str):
+    leaf = qkv.detach().clone().requires_grad_(phase == "step")
 
+    def fwd():
+        with torch.no_grad():
+            c.forward(leaf)
 
-def make_inputs(path: Path, b: int, h: int, s: int, seed: int) -> None:
-    import torch
-    from safetensors.torch import save_file
-    g = torch.Generator().manual_seed(seed)
-    hd = h * HEAD_DIM
-    save_file({"qkv": torch.randn(b, s, 3 * hd, generator=g),
-               "dout": torch.randn(b, s, hd, generator=g)}, str(path))
+    def step():
+        leaf.grad = None
+        c.forward(leaf).backward(dout)
 
-
-def score(out: Path, names: list[str], heads: int, causal: bool) -> dict[str, dict]:
-    """Every candidate's o, dq, dk, dv against an fp64 CPU recompute; plus the fp32 floor."""
-    import torch
-    from safetensors.torch import load_file
-    t = load_file(str(out / "data" / "inputs.safetensors"))
-    qkv = t["qkv"].double().requires_grad_(True)
-    o = composed(qkv, heads, 1.0 / HEAD_DIM ** 0.5, causal)
-    (o * t["dout"].double()).sum().backward()
-
-    def parts(o_, g_):
-        dq, dk, dv = g_.chunk(3, dim=-1)
-        return {"o": o_, "dq": dq, "dk": dk, "dv": dv}
-
-    ref = parts(o.detach(), qkv.grad)
-
-    def errors(got):
-        res = {}
-        for p in PARTS:
-            diff = got[p].double() - ref[p]
-            res[p] = {"max_abs": diff.abs().max().item(),
-                      "rel_fro": (diff.norm() / ref[p].norm()).item()}
-        return res
-
-    scores = {"fp64_rounded_to_fp32": errors({p: ref[p].float() for p in PARTS})}
-    for name in names:
-        c = load_file(str(out / "data" / f"{name}.safetensors"))
-        scores[name] = errors(parts(c["o"], c["dqkv"]))
-    return scores
+    return fwd if phase == "fwd" else step
 
 
-def collect_wall(out: Path, rounds: int) -> dict:
-    """wall[name][phase] = round medians (ms per call); net = train - head within a round."""
-    wall: dict = {}
+def event_block(torch, fn, calls: int) -> float:
+    """ms per call over `calls` back-to-back calls, between two HIP events."""
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(calls):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / calls
+
+
+def measure(torch, live: list[Contender], qkv, dout, rounds: int, reps: int, calls: int,
+            warmup: int, log=print) -> dict:
+    """{contender: {phase: [round values]}}, rounds ordered by the cyclic Latin square."""
+    fns = {(c.name, p): phase_fn(torch, c, qkv, dout, p) for c in live for p in PHASES}
+    for fn in fns.values():
+        for _ in range(warmup):
+            fn()
+    torch.cuda.synchronize()
+    by_name = {c.name: c for c in live}
+    res = {c.name: {p: [] for p in PHASES} for c in live}
     for r in range(rounds):
-        rows = json.loads((out / f"time_r{r}.json").read_text(encoding="utf-8"))
-        med = {(x["name"], x["phase"]): statistics.median(x["ms"]) for x in rows}
-        head = med[("head", "head")]
-        for (name, phase), m in med.items():
-            w = wall.setdefault(name, {})
-            w.setdefault(phase, []).append(m)
-            if phase == "train":
-                w.setdefault("net", []).append(m - head)
-    return wall
+        samples = {k: [] for k in fns}
+        for _ in range(reps):
+            for name in latin_row([c.name for c in live], r):
+                for p in PHASES:
+                    samples[(name, p)].append(event_block(torch, fns[(name, p)], calls))
+        for (name, p), xs in samples.items():
+            res[name][p].append(round_value(xs))
+        log(f"compare: round {r + 1}/{rounds}: " + ", ".join(
+            f"{n} {res[n]['step'][-1]:.4f}" for n in by_name))
+    return res
 
 
-def run(a) -> None:
-    out = a.out.resolve()
-    out.mkdir(parents=True, exist_ok=True)
-    log(f"output: {out}")
-    (out / "data").mkdir(exist_ok=True)
-    inputs = out / "data" / "inputs.safetensors"
-    make_inputs(inputs, a.batch, a.heads, a.seq, a.seed)
-    me = [sys.executable, "-m", "candle_fused_attn.compare", "side"]
-    common = ["--inputs", str(inputs), "--out", str(out), "--heads", str(a.heads)]
-    common += ["--causal"] if a.causal else []
-    env = dict(os.environ)
-    pkg = str(Path(__file__).resolve().parent.parent)
-    env["PYTHONPATH"] = pkg + os.pathsep + env.get("PYTHONPATH", "")
-
-    log("accuracy + determinism (GPU)")
-    subprocess.run(me + ["accuracy"] + common, check=True, env=env, timeout=600)
-    acc = json.loads((out / "accuracy.json").read_text(encoding="utf-8"))
-    names = [r["name"] for r in acc["candidates"]]
-    scores = score(out, names, a.heads, a.causal)
-
-    for r in range(a.rounds):
-        log(f"round {r + 1}/{a.rounds} (GPU)")
-        subprocess.run(me + ["time"] + common + [
-            "--round", str(r), "--samples", str(a.samples), "--calls", str(a.calls),
-            "--warmup", str(a.warmup), "--names", json.dumps(names)], check=True, env=env,
-            timeout=900)
-    wall = collect_wall(out, a.rounds)
-
-    kernels: dict = {}
-    prof = shutil.which("rocprofv3") if a.kernels else None
-    if a.kernels and not prof:
-        log("kernel pass SKIPPED: no rocprofv3 on PATH")
-    if prof:
-        jobs = [(n, p) for n in names for p in ("fwd", "train")] + [("head", "head")]
-        for i, (name, phase) in enumerate(jobs):
-            log(f"rocprofv3 {i + 1}/{len(jobs)}: {name} {phase} (GPU)")
-            d = out / f"prof_{name}_{phase}"
-            cmd = [prof, "--kernel-trace", "--stats", "--output-format", "csv", "-d", str(d),
-                   "-o", "run", "--", sys.executable, "-m", "candle_fused_attn.compare", "side",
-                   "kernels"] + common + ["--only", name, "--phase", phase,
-                                          "--calls", str(a.kernel_calls)]
-            subprocess.run(cmd, check=True, env=env, capture_output=True, timeout=600)
-            stats = next(d.rglob("run_kernel_stats.csv")).read_text(encoding="utf-8")
-            kernels[f"{name}:{phase}"] = per_call(kernel_rows(stats), a.kernel_calls)
-
-    report = {"env": {"date": time.strftime("%Y-%m-%d %H:%M:%S"),
-                      "shape": [a.batch, a.heads, a.seq, HEAD_DIM], "causal": a.causal,
-                      "seed": a.seed, "timing": {"rounds": a.rounds, "samples": a.samples,
-                                                  "calls": a.calls, "warmup": a.warmup,
-                                                  "kernel_calls": a.kernel_calls}},
-              "device": acc["env"], "status": acc["status"],
-              "deterministic": {r["name"]: r["deterministic"] for r in acc["candidates"]},
-              "accuracy": scores, "wall": wall, "kernels": kernels}
-    (out / "report.json").write_text(json.dumps(report, indent=1), encoding="utf-8")
-    md = render(report, names)
-    (out / "report.md").write_text(md, encoding="utf-8")
-    if not a.keep_data:
-        shutil.rmtree(out / "data", ignore_errors=True)
-    print(md)
+def kernel_probe(args) -> None:
+    """Child mode (run under rocprofv3): `calls` calls of one contender and phase, nothing else
+    (the parent keeps the last ones: the first of a fresh process run at ramping clocks)."""
+    import torch
+    data = torch.load(args.inputs, weights_only=True)
+    qkv, dout = data["qkv"].cuda(), data["dout"].cuda()
+    c = {x.name: x for x in make_contenders(args.heads, args.scale, args.causal)}[args.contender]
+    fn = phase_fn(torch, c, qkv, dout, args.phase)
+    for _ in range(args.calls):
+        fn()
+    torch.cuda.synchronize()
 
 
-def render(rep: dict, names: list[str]) -> str:
-    """The Markdown report."""
-    e, d = rep["env"], rep["device"]
-    lines = [f"# fused attention vs PyTorch-ROCm fp32 attention — {e['date']}", "",
-             f"{d['gpu']} ({d['arch']}, {d['cus']} CUs); torch {d['torch']} (HIP {d['hip']}), "
-             f"fp32 matmul precision `{d['fp32_matmul_precision']}`; {d.get('libfattn', '')}. "
-             f"Shape b·h·s·d = {' · '.join(map(str, e['shape']))}, causal {e['causal']}, "
-             f"seed {e['seed']}. Timing: {e['timing']}.", "",
-             "## Candidates on these inputs (forward + backward once)", ""]
-    lines += [f"- `{k}`: {v}" for k, v in rep["status"].items()]
-    lines += ["", "## Accuracy against fp64 (normwise relative error; max-abs in brackets)", "",
-              "| candidate | o | dq | dk | dv | 2 runs bitwise equal |",
-              "|---|---|---|---|---|---|"]
-    for name, s in rep["accuracy"].items():
-        cells = [f"{s[p]['rel_fro']:.2e} [{s[p]['max_abs']:.1e}]" for p in PARTS]
-        lines.append(f"| {name} | " + " | ".join(cells) +
-                     f" | {rep['deterministic'].get(name, '—')} |")
-    lines += ["", "## Wall time, ms per call: median of round medians [min–max over rounds]", "",
-              "| candidate | fwd | train | net = train − head |", "|---|---|---|---|"]
-    for name in names:
-        w = rep["wall"][name]
-        lines.append(f"| {name} | " + " | ".join(fmt_range(w.get(p, [])) for p in PHASES) + " |")
-    lines.append(f"| (head) | | {fmt_range(rep['wall']['head']['head'])} | |")
-    ours = names[0]
-    lines += ["", f"Decision rule against `{ours}` (worst round of one < best round of the "
-              "other):", ""]
-    for name in names[1:]:
-        cells = [f"{p}: {verdict(ours, rep['wall'][ours][p], name, rep['wall'][name][p])}"
-                 for p in PHASES]
-        lines.append(f"- vs `{name}` — " + "; ".join(cells))
-    k = rep["kernels"]
-    if k:
-        lines += ["", "## Kernel time (rocprofv3), ms per call", "",
-                  "| candidate | fwd | train | net = train − head | irregular kernels |",
-                  "|---|---|---|---|---|"]
-        for name in names:
-            f, t = k[f"{name}:fwd"], k[f"{name}:train"]
-            net = t["ms"] - k["head:head"]["ms"]
-            irr = sorted(set(f["irregular"]) | set(t["irregular"]))
-            lines.append(f"| {name} | {f['ms']:.3f} | {t['ms']:.3f} | {net:.3f} | "
-                         f"{', '.join(short_name(x)[:60] for x in irr) or '—'} |")
-        lines += ["", "Kernels per train call (launches per call × µs per call):", ""]
-        for name in names:
-            ks = sorted(k[f"{name}:train"]["kernels"], key=lambda x: -x["us_per_call"])
-            lines.append(f"- `{name}`: " + "; ".join(
-                f"{short_name(x['name'])[:70]} ×{x['per_call']:g} {x['us_per_call']:.1f}"
-                for x in ks))
+def profile_kernels(args, name: str, phase: str, inputs: Path, work: Path) -> dict | None:
+    rocprof = shutil.which("rocprofv3")
+    if rocprof is None:
+        return None
+    tag = f"{name.replace('.', '_')}_{phase}"
+    skip = args.kernel_skip
+    cmd = [rocprof, "--kernel-trace", "--output-format", "csv", "-d", str(work / tag),
+           "-o", "run", "--", sys.executable, "-m", "candle_fused_attn.compare", "probe",
+           "--inputs", str(inputs), "--contender", name, "--phase", phase,
+           "--calls", str(skip + args.kernel_calls), "--heads", str(args.heads),
+           "--scale", str(args.scale)] + (["--causal"] if args.causal else [])
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    trace = sorted((work / tag).rglob("*kernel_trace.csv"))
+    if not trace:
+        return {"ms": None, "kernels": [], "other": [],
+                "error": (res.stderr or res.stdout)[-400:]}
+    rows = parse_kernel_trace(trace[0].read_text(), skip, args.kernel_calls)
+    return kernel_time_per_call(rows, args.kernel_calls)
+
+
+# --- the report ---------------------------------------------------------------------------------
+
+def render(rep: dict) -> str:
+    """The markdown report from the JSON result."""
+    s = rep["setup"]
+    lines = [f"# fused attention vs PyTorch-ROCm fp32 attention on {s['device']}", "",
+             f"qkv [{s['b']}, {s['s']}, {3 * s['h'] * s['d']}] (h {s['h']}, d {s['d']}), "
+             f"dout [{s['b']}, {s['s']}, {s['h'] * s['d']}], N(0, 1) from a CPU generator seeded "
+             f"{s['seed']}, scale {s['scale']:g}, {'causal' if s['causal'] else 'non-causal'}. "
+             f"{s['when']}; torch {s['torch']}, HIP {s['hip']}, fp32 matmul precision "
+             f"{s['matmul_precision']}.", "",
+             "## Contenders", "", "| name | what | status |", "|---|---|---|"]
+    for name, st in rep["status"].items():
+        lines.append(f"| {name} | {rep['what'][name]} | {st} |")
+    live = [n for n, st in rep["status"].items() if st == "ran"]
+    lines += ["", "## Agreement with float64 (normwise relative error / max-abs)", "",
+              "| name | o | dq | dk | dv | rerun bit-equal |", "|---|--:|--:|--:|--:|:-:|"]
+    for name in ["float64 rounded to fp32"] + live:
+        e = rep["agreement"][name]
+        cells = [f"{e[p]['rel']:.2e} / {e[p]['max_abs']:.1e}" for p in PARTS]
+        eq = rep["rerun_equal"].get(name)
+        lines.append(f"| {name} | " + " | ".join(cells) + f" | {'' if eq is None else ('yes' if eq else 'no')} |")
+    t = rep["timing"]
+    lines += ["", f"## Time per call, HIP events (ms; median over {t['rounds']} rounds, range)", "",
+              f"Each round: {t['reps']} samples of {t['calls']} back-to-back calls per contender "
+              f"and phase after {t['warmup']} warm-up calls, contenders ordered by one row of a "
+              "cyclic Latin square; a round's value is its samples' median. `step` = forward + "
+              "backward.", "", "| name | fwd | step |", "|---|--:|--:|"]
+    for name in live:
+        lines.append(f"| {name} | {spread(t['ms'][name]['fwd'])} | {spread(t['ms'][name]['step'])} |")
+    lines += ["", "Head to head (A ahead when faster in every round):", "",
+              "| A | B | fwd | step |", "|---|---|---|---|"]
+    for a in MINE:
+        for b in live:
+            if b in MINE or a not in live:
+                continue
+            cells = [head_to_head(a, t["ms"][a][p], b, t["ms"][b][p]) for p in PHASES]
+            lines.append(f"| {a} | {b} | " + " | ".join(cells) + " |")
+    if rep.get("kernels"):
+        lines += ["", f"## Kernel time per call, rocprofv3 (the last {rep['kernel_calls']} of "
+                  f"{rep['kernel_skip'] + rep['kernel_calls']} calls per probe)",
+                  "", "| name | phase | ms | kernels (launches per call, us per call) | not per call |",
+                  "|---|---|--:|---|---|"]
+        for key, k in rep["kernels"].items():
+            name, phase = key.rsplit(":", 1)
+            if k is None or k.get("ms") is None:
+                lines.append(f"| {name} | {phase} | n/a | {(k or {}).get('error', 'no profiler')} | |")
+                continue
+            ks = "; ".join(f"{short_kernel(x['name'])} x{x['per_call']} {x['us']:.1f}"
+                           for x in k["kernels"][:6])
+            lines.append(f"| {name} | {phase} | {k['ms']:.4f} | {ks} | "
+                         + ", ".join(short_kernel(o) for o in k["other"]) + " |")
     return "\n".join(lines) + "\n"
 
 
-def main(argv=None) -> None:
-    p = argparse.ArgumentParser(description=__doc__,
-                                formatter_class=argparse.RawDescriptionHelpFormatter)
-    p.add_argument("command", choices=["run", "side"])
-    p.add_argument("mode", nargs="?", choices=["accuracy", "time", "kernels"], help="side only")
-    p.add_argument("--batch", type=int, default=64)
-    p.add_argument("--heads", type=int, default=6)
-    p.add_argument("--seq", type=int, default=240)
-    p.add_argument("--causal", action="store_true")
-    p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--rounds", type=int, default=3)
-    p.add_argument("--samples", type=int, default=15)
-    p.add_argument("--calls", type=int, default=10, help="back-to-back calls per sample")
-    p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--kernels", action="store_true", help="also the rocprofv3 kernel pass")
-    p.add_argument("--kernel-calls", type=int, default=20)
-    p.add_argument("--out", type=Path, default=Path("gpurun_out/compare"))
-    p.add_argument("--keep-data", action="store_true", help="keep the inputs and outputs")
-    # The child's arguments.
-    p.add_argument("--inputs", type=Path)
-    p.add_argument("--round", type=int, default=0)
-    p.add_argument("--names", type=str, default="[]")
-    p.add_argument("--only", type=str)
-    p.add_argument("--phase", type=str)
-    a = p.parse_args(argv)
-    if a.command == "run":
-        run(a)
-    else:
-        {"accuracy": side_accuracy, "time": side_time, "kernels": side_kernels}[a.mode](a)
+def report(args) -> int:
+    import torch
+
+    out = Path(args.out)
+    out.mkdir(parents=True, exist_ok=True)
+    torch.set_float32_matmul_precision("highest")
+    dev = torch.device("cuda:0")
+    b, h, s, d = args.batch, args.heads, args.seq, 64
+    g = torch.Generator().manual_seed(args.seed)
+    qkv_cpu = torch.randn(b, s, 3 * h * d, generator=g)
+    dout_cpu = torch.randn(b, s, h * d, generator=g)
+    qkv, dout = qkv_cpu.to(dev), dout_cpu.to(dev)
+    log = lambda m: print(m, file=sys.stderr, flush=True)  # noqa: E731
+
+    ref = reference64(qkv_cpu, dout_cpu, h, args.scale, args.causal)
+    props = torch.cuda.get_device_properties(dev)
+    device = f"{props.gcnArchName.split(':')[0]} ({props.multi_processor_count} CUs)"
+    rep = {"setup": {"device": device, "b": b, "h": h, "s": s, "d": d,
+                     "seed": args.seed, "scale": args.scale, "causal": args.causal,
+                     "when": time.strftime("%Y-%m-%d %H:%M"), "torch": torch.__version__,
+                     "hip": torch.version.hip,
+                     "matmul_precision": torch.get_float32_matmul_precision()},
+           "status": {}, "what": {}, "rerun_equal": {},
+           "agreement": {"float64 rounded to fp32": agreement(
+               {p: v.float() for p, v in ref.items()}, ref)}}
+    contenders = make_contenders(h, args.scale, args.causal)
+    live = []
+    for c in contenders:
+        rep["what"][c.name] = c.what
+        try:
+            first = one_step(c, qkv, dout)
+            second = one_step(c, qkv, dout)
+            torch.cuda.synchronize()
+        except Exception as e:  # a backend that refuses these inputs is recorded, not timed
+            rep["status"][c.name] = "refused: " + str(e).splitlines()[0][:160]
+            torch.cuda.synchronize()
+            continue
+        rep["status"][c.name] = "ran"
+        rep["agreement"][c.name] = agreement(dict(zip(PARTS, first)), ref)
+        rep["rerun_equal"][c.name] = all(
+            torch.equal(x.contiguous().view(torch.int32), y.contiguous().view(torch.int32))
+            for x, y in zip(first, second))
+        live.append(c)
+        log(f"compare: {c.name}: " + " ".join(
+            f"{p} {rep['agreement'][c.name][p]['rel']:.2e}" for p in PARTS))
+    rep["timing"] = {"rounds": args.rounds, "reps": args.reps, "calls": args.calls,
+                     "warmup": args.warmup,
+                     "ms": measure(torch, live, qkv, dout, args.rounds, args.reps, args.calls,
+                                   args.warmup, log)}
+    if args.kernels:
+        rep["kernel_calls"], rep["kernel_skip"] = args.kernel_calls, args.kernel_skip
+        rep["kernels"] = {}
+        with tempfile.TemporaryDirectory(dir=out) as tmp:
+            work = Path(tmp)
+            inputs = work / "inputs.pt"
+            torch.save({"qkv": qkv_cpu, "dout": dout_cpu}, inputs)
+            for c in live:
+                for p in PHASES:
+                    log(f"compare: rocprofv3 {c.name} {p}")
+                    rep["kernels"][f"{c.name}:{p}"] = profile_kernels(args, c.name, p, inputs,
+                                                                      work)
+    (out / "report.json").write_text(json.dumps(rep, indent=1) + "\n")
+    (out / "report.md").write_text(render(rep))
+    log(f"compare: wrote {out / 'report.md'}")
+    return 0
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(prog="python -m candle_fused_attn.compare",
+                                 description="fused attention vs PyTorch-ROCm fp32 attention")
+    sub = ap.add_subparsers(dest="mode", required=True)
+    r = sub.add_parser("report", help="measure every contender and write the report")
+    r.add_argument("--out", required=True)
+    r.add_argument("--batch", type=int, default=64)
+    r.add_argument("--seq", type=int, default=240)
+    r.add_argument("--seed", type=int, default=0)
+    r.add_argument("--rounds", type=int, default=4)
+    r.add_argument("--reps", type=int, default=5, help="samples per contender, phase and round")
+    r.add_argument("--calls", type=int, default=20, help="back-to-back calls per sample")
+    r.add_argument("--warmup", type=int, default=50)
+    r.add_argument("--kernels", action="store_true", help="rocprofv3 kernel time per call")
+    r.add_argument("--kernel-calls", type=int, default=100, help="calls kept per probe")
+    # A fresh process's first ~100 calls run at ramping clocks: the probe's first calls are run
+    # and dropped.
+    r.add_argument("--kernel-skip", type=int, default=200, help="calls dropped per probe")
+    p = sub.add_parser("probe", help="(child of --kernels) run one contender and phase")
+    p.add_argument("--inputs", required=True)
+    p.add_argument("--contender", required=True)
+    p.add_argument("--phase", choices=PHASES, required=True)
+    p.add_argument("--calls", type=int, default=20)
+    for q in (r, p):
+        q.add_argument("--heads", type=int, default=6)
+        q.add_argument("--scale", type=float, default=0.125)
+        q.add_argument("--causal", action="store_true")
+    args = ap.parse_args(argv)
+    if args.mode == "probe":
+        kernel_probe(args)
+        return 0
+    return report(args)
 
 
 if __name__ == "__main__":
-    main()
+    sys.exit(main())
