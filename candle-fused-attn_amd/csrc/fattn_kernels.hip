@@ -1108,8 +1108,9 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
       if (!live[m]) continue;
       const f4 Lv = ld4(&sL[buf][16 * m + 4 * g]), Dv = ld4(&sD[buf][16 * m + 4 * g]);
       const int qi0 = q0 + 16 * m + 4 * g;
-      if (!a.causal && q0 + 16 * m + 16 <= S && kw0 + 16 <= S) {
-        // Every query and key of the subtile is live (wave-uniform test): no mask.
+      if ((!a.causal || kw0 + 15 <= q0 + 16 * m) && q0 + 16 * m + 16 <= S && kw0 + 16 <= S) {
+        // Every query and key of the subtile is live (wave-uniform test; causal: every key at or
+        // before every query): no mask.
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float p = exp2_hw(fmaf(sS[m][r], a.scale, -Lv[r]) * kLog2e);
@@ -1560,7 +1561,8 @@ bwd_split_kernel(BwdArgs a) {
       // key `key`. Then dV^T and dK^T.
       const f4 Lv = ld4(&sL[buf][4 * g]), Dv = ld4(&sD[buf][4 * g]);
       const int qi0 = q0 + 4 * g;
-      if (!a.causal && q0 + 16 <= S && kw0 + 16 <= S) {
+      if ((!a.causal || kw0 + 15 <= q0) && q0 + 16 <= S && kw0 + 16 <= S) {
+        // Every query and key live (causal: every key at or before every query): no mask.
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float p = exp2_hw(fmaf(sS[r], a.scale, -Lv[r]) * kLog2e);
