@@ -437,12 +437,16 @@ fwd_kernel(FwdArgs a) {
   }
 
   stage(0, Const<0>{});
+  // Negated for a negative scale, zero past S (wave-uniform test: most waves need neither).
+  const bool q_fix = a.scale < 0.0f || qw0 + kFwdWaveQ > S;
 #pragma unroll
   for (int n = 0; n < kFwdNT; ++n) {
     const int qi = qw0 + 16 * n + lo;
     quarter_place<D>(qload[n], qr[n]);
+    if (q_fix) {
 #pragma unroll
-    for (int t = 0; t < kQR; ++t) qr[n][t] = qi < S ? qr[n][t] * qsign : 0.0f;
+      for (int t = 0; t < kQR; ++t) qr[n][t] = qi < S ? qr[n][t] * qsign : 0.0f;
+    }
   }
   wait_mem();
   __syncthreads();
@@ -1514,10 +1518,12 @@ bwd_split_kernel(BwdArgs a) {
   if (nsteps > 1) gload(1, Const<1>{});
   quarter_place<D>(kload, kB);
   quarter_place<D>(vload, vB);
+  if (kw0 + 16 > S) {  // wave-uniform: only a wave with keys past S zeroes them
 #pragma unroll
-  for (int t = 0; t < kKR; ++t) {
-    kB[t] = key < S ? kB[t] : 0.0f;
-    vB[t] = key < S ? vB[t] : 0.0f;
+    for (int t = 0; t < kKR; ++t) {
+      kB[t] = key < S ? kB[t] : 0.0f;
+      vB[t] = key < S ? vB[t] : 0.0f;
+    }
   }
   wait_mem();  // the direct copies have landed
   __syncthreads();
