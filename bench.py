@@ -447,7 +447,8 @@ def main() -> int:
             if cfg == main_cfg:
                 continue
             xw = Workload(torch, L, _lib, dev, cfg)
-            extra[f"config{cfg}"] = time_extra(torch, xw, max(args.extra_steps, 1), 3)
+            # 25 warm-up steps: the first calls on a new shape touch freshly allocated pages.
+            extra[f"config{cfg}"] = time_extra(torch, xw, max(args.extra_steps, 1), 25)
             log(f"bench: {CONFIGS[cfg][0]}: {json.dumps(extra[f'config{cfg}'])}")
             del xw
             torch.cuda.empty_cache()
