@@ -667,6 +667,10 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
   return 0;
 }
 
+// Test hook (not declared in include/fattn.h): step 2's dQ sums on (1, the default) or off (0:
+// step 3 sums every tile) for every later backward of the process. Returns the previous setting.
+int fattn_internal_step2_sums(int on) { return fattn::set_step2_sums(on != 0) ? 1 : 0; }
+
 int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                      int64_t s, void* stream, int* status) {
   if (!status) return fail(FATTN_EINVAL, "fused_attention: null status");

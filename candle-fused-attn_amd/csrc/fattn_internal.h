@@ -104,6 +104,9 @@ __host__ __device__ inline bool sum_target(SumPlan p, int x, int m, int BH, int 
 }
 // Workgroups appended to step 2's grid for these sums (0: step 3 sums every tile).
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal);
+// Step 2's sums on (the default) or off for every later backward of the process, so that a test
+// can compare both; returns the previous setting.
+bool set_step2_sums(bool on);
 // Step 3's grid: one workgroup per query tile, or (with step 2's sums) at most 256 workgroups
 // that each check a range of tiles and sum those not done.
 int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal);

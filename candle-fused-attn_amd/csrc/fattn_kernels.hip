@@ -771,11 +771,10 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   // fit beside the others.
   constexpr bool kKtLds = D == 128;
   __shared__ __attribute__((aligned(16))) float sKt[kKtLds ? D * kBwdLd : 4];
+  // D always comes from step 1 here (the split mode at D <= 64 runs bwd_split_kernel, which
+  // forms D itself).
+  static_assert(!kSplit || D == 128, "the split mode at D <= 64 is bwd_split_kernel");
   __shared__ __attribute__((aligned(16))) float sQ[2][kQT * D];
-  // split (D <= 64): the O tile, for D = rowsum(dO o O) computed here (step 1 computes it for the
-  // turn mode, and for D 128, whose LDS has no room for O).
-  constexpr bool kFuseD = kSplit && D <= 64;
-  __shared__ __attribute__((aligned(16))) float sO[kFuseD ? 2 : 1][kFuseD ? kQT * D : 4];
   __shared__ __attribute__((aligned(16))) float sdO[2][kQT * D];
   // dS [kQT][64 keys], swizzled like a D 64 tile (its writes are column reads' pattern, its
   // reads row-wise float4 reads).
@@ -829,9 +828,6 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   const float* kp = a.k.p + b * a.k.sb + h * a.k.sh;
   const float* vp = a.v.p + b * a.v.sb + h * a.v.sh;
   const float* gp = a.d_o.p + b * a.d_o.sb + h * a.d_o.sh;
-  // O [b, s, h, D]: row i of this (b, h) at op + i H D (split only).
-  const float* op = kFuseD ? a.o + (static_cast<int64_t>(b) * S * a.H + h) * D : nullptr;
-  const unsigned o_ss4 = static_cast<unsigned>(a.H) * D * 4u;
   const float* lp = a.lse + static_cast<int64_t>(bh) * S;
   const float* dp = a.dsum + static_cast<int64_t>(bh) * S;
   int* tp = a.turn + static_cast<int64_t>(bh) * a.ntile;
@@ -887,34 +883,13 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
       if (j0 + w < kCopies) {
         copy_part<D>(qp, q_ss4, q0, S - 1, sQ[buf], j0 + w, lane);
         copy_part<D>(gp, g_ss4, q0, S - 1, sdO[buf], j0 + w, lane);
-        if constexpr (kFuseD) copy_part<D>(op, o_ss4, q0, S - 1, sO[buf], j0 + w, lane);
       }
     }
-    if (kFuseD ? w == 0 : w < 2) {
+    if (w < 2) {
       if (lane < kQT) {
         const unsigned off = 4u * static_cast<unsigned>(min(q0 + lane, S - 1));
         load_lds4(w == 0 ? lp : dp, off, w == 0 ? sL[buf] : sD[buf]);
       }
-    }
-  };
-  // kFuseD: D of the tile in buffer `buf` from its staged O and dO rows, into sD[buf]. D / 4 lanes
-  // per row, the same operations in the same order as step 1 (prep_kernel), so D is the same.
-  auto rowsum_do_o = [&](int buf) {
-    constexpr int kLanes = D / 4;
-#pragma unroll
-    for (int i0 = 0; i0 < kQT * kLanes; i0 += kThreads) {
-      const int i = i0 + tid, row = i / kLanes, c4 = i % kLanes;
-      float x = 0.0f;
-      if (i < kQT * kLanes) {
-        const f4 ov = ld4(&sO[kFuseD ? buf : 0][swz<D>(row, 4 * c4)]);
-        const f4 gv = ld4(&sdO[buf][swz<D>(row, 4 * c4)]);
-        x = ov.x * gv.x;
-        x = fmaf(ov.y, gv.y, x);
-        x = fmaf(ov.z, gv.z, x);
-        x = fmaf(ov.w, gv.w, x);
-      }
-      x = lane_sum<kLanes>(x);
-      if (i < kQT * kLanes && c4 == 0) sD[buf][row] = x;
     }
   };
   // The order in which key blocks add into a tile's dQ (fixed by the shape alone, so every run
@@ -1045,10 +1020,6 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   gload(tile_at(0) * kQT, 0);
   wait_stores();  // the direct copies have landed
   __syncthreads();
-  if constexpr (kFuseD) {
-    rowsum_do_o(0);
-    __syncthreads();
-  }
   // One tile; `bufc()` is the LDS buffer, t % 2. The split kernel unrolls the walk by two so that
   // it is a compile-time constant there and LDS addresses fold the buffer offset into the
   // instruction (the turn kernel has no registers to spare for that).
@@ -1209,10 +1180,7 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
     p1_q0 = q0;
     p1_pos = pos_of(q0 / kQT);
     p1_cnt = count_of(q0 / kQT);
-    if constexpr (kFuseD) {
-      if (has_next) rowsum_do_o(buf ^ 1);  // the next tile's D (its rows landed before the barrier)
-    }
-    __syncthreads();  // dS read by every wave; the next tile's D written
+    __syncthreads();  // dS read by every wave
   };
   if constexpr (kSplit) {
     for (int t = 0; t < nsteps; t += 2) {
@@ -1826,7 +1794,13 @@ int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d) {
 }
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQT - 1) / kQT); }
 bool bwd_needs_prep(bool split, int d) { return !split || d > 64; }
+namespace {
+std::atomic<int> g_step2_sums{1};
+}  // namespace
+bool set_step2_sums(bool on) { return g_step2_sums.exchange(on ? 1 : 0) != 0; }
+
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  if (g_step2_sums.load(std::memory_order_relaxed) == 0) return 0;
   // The range check keeps b h s (hence every count below) inside int32.
   const int nkb = static_cast<int>((s + kBwdKeys - 1) / kBwdKeys);
   const int ntile = static_cast<int>((s + kQT - 1) / kQT);

@@ -708,6 +708,32 @@ def step2_summed_tiles(qkv, dout, h, d, causal, grad_want):
     return done == epoch
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_step2_sums_equal_step3_sums_at_scale(orc, cuda, causal):
+    """Step 2's tail sums read the partials of key blocks that ran on their own XCD, from that
+    XCD's L2, with plain loads after an agent-scope arrival flag; step 3 reads them after a kernel
+    boundary. At config 2's shape (384 heads, every tile summed in step 2), the backward with step
+    2's sums switched off (step 3 sums every tile) must give the same bits, on three runs."""
+    L = _lib.lib()
+    f = L.fattn_internal_step2_sums
+    f.argtypes = [ctypes.c_int]
+    f.restype = ctypes.c_int
+    x, dout, qkv, g = seeded_qkv(orc, 64, 6, 240, 5, cuda)
+    res = {}
+    for on in (1, 0, 1, 0, 1, 0):
+        prev = f(on)
+        try:
+            _, grad = run("fused_qkv", qkv, g, 6, 64, causal, 0.125)
+        finally:
+            f(prev)
+        b = bits(grad)
+        if on in res:
+            assert torch.equal(b, res[on]), f"step 2 sums {'on' if on else 'off'}: reruns differ"
+        res[on] = b
+    say(f"  causal={causal}: step 2 sums on == off: {torch.equal(res[1], res[0])}")
+    assert torch.equal(res[1], res[0])
+
+
 @pytest.mark.parametrize("d", [32, 64])
 def test_causal_dq_sums_match_turns(orc, cuda, d):
     """Causal split backward with 8 | b h (step 2's last workgroups sum the dQ tiles, each waiting
