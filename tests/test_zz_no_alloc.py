@@ -84,3 +84,67 @@ def test_noalloc_refuses_what_does_not_fit(cuda):
                                  st, st, None)
     assert rc == _lib.FATTN_EWORKSPACE
     assert "static scratch" in _lib.last_error()
+
+
+@pytest.mark.parametrize("shape", [(64, 6, 240), (4, 6, 240)])
+def test_noalloc_under_graph_capture(cuda, shape):
+    """The no-alloc backward is for callers under HIP graph capture: the forward and
+    fattn_bwd_f32_noalloc captured in one graph and replayed on new inputs (with eager work and
+    synchronisations between replays) equal eager fattn_bwd_f32 runs with a workspace of the kind
+    the no-alloc entry picks (config 2's shape: turns; the smaller one: split), bit for bit."""
+    b, h, s = shape
+    d = 64
+    L = _lib.lib()
+    qkv = torch.empty(b, s, 3 * h * d, device=cuda)
+    dout = torch.empty(b, s, h * d, device=cuda)
+    o = torch.empty(b, s, h * d, device=cuda)
+    lse = torch.empty(b, h, s, device=cuda)
+    got = torch.empty_like(qkv)
+    st = _lib.arr([s * 3 * h * d, d, 3 * h * d])
+    gst = _lib.arr([s * h * d, d, h * d])
+    qp, kp, vp = (ctypes.c_void_p(qkv.data_ptr() + i * h * d * 4) for i in range(3))
+    split = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
+    n = split if split <= STATIC_SCRATCH else L.fattn_bwd_workspace_min_bytes(b, h, s, d)
+    ws = torch.empty(n, dtype=torch.uint8, device=cuda)
+
+    def captured():
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(L.fattn_fwd_f32(qp, kp, vp, P(o), P(lse), b, h, s, d, 0.125, 0, st, st, st,
+                                   stream))
+        _lib.check(L.fattn_bwd_f32_noalloc(qp, kp, vp, P(o), P(dout), P(lse), P(got), b, h, s,
+                                           d, 0.125, 0, st, st, st, gst, stream))
+
+    def eager_reference():
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        want = torch.empty_like(qkv)
+        _lib.check(L.fattn_fwd_f32(qp, kp, vp, P(o), P(lse), b, h, s, d, 0.125, 0, st, st, st,
+                                   stream))
+        _lib.check(L.fattn_bwd_f32(qp, kp, vp, P(o), P(dout), P(lse), P(want), P(ws), n, b, h, s,
+                                   d, 0.125, 0, st, st, st, gst, stream))
+        torch.cuda.synchronize()
+        return want
+
+    gen = torch.Generator().manual_seed(21)
+    qkv.copy_(torch.randn(qkv.shape, generator=gen))
+    dout.copy_(torch.randn(dout.shape, generator=gen))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        captured()  # warm-up (the scratch's address is looked up here, outside the capture)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured()
+    for r in range(3):
+        say(f"noalloc graph replay {r} shape {shape} ({'split' if n == split else 'turns'})")
+        qkv.copy_(torch.randn(qkv.shape, generator=gen))
+        dout.copy_(torch.randn(dout.shape, generator=gen))
+        got.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        g = got.clone()
+        want = eager_reference()
+        assert torch.isfinite(want).all()
+        assert torch.equal(g.view(torch.int32), want.view(torch.int32)), f"replay {r}"
