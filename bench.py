@@ -11,12 +11,20 @@ timed region. The op-level C ABI is called with preallocated outputs on torch's 
 Configs 3-5 (causal, long causal, strided views) are timed too, as extra keys of the same line
 (`configs`): op-level forward and forward+backward, and each kernel on its own.
 
+Order of the GPU work: W warm-up + K timed steps from an idle GPU (`fwd_bwd_from_idle_ms`),
+configs 3-5, then W warm-up + K timed steps (`value`), K forwards (`fwd_ms`) and K kernel-level
+steps (`kernels_us`, `roofline`). MI355X runs at lower clocks for some tens of milliseconds after
+an idle second, so the headline steps come right after sustained work, as in a training loop; the
+from-idle figure shows what a short run on an idle GPU sees.
+
 Prints ONE JSON line. `--gpus N` with N > 1 exits: this build runs on one GPU.
 
 `--traffic-from FETCH_CSV WRITE_CSV` does not touch a GPU: it turns two `rocprofv3 --pmc
 FETCH_SIZE` / `--pmc WRITE_SIZE` counter files of a `--calibrate-copy` run into
 profiles/traffic.json (HBM bytes per launch, scaled by the 256 MiB copy's counters, tagged with
-the sha256 of the libfattn.so that was measured).
+the sha256 of the libfattn.so that was measured). `--trace-from KERNEL_TRACE_CSV` (no GPU either)
+prints the per-kernel durations of the headline's timed and kernel-level steps from a
+`rocprofv3 --kernel-trace` file of the same command.
 """
 from __future__ import annotations
 
@@ -276,6 +284,66 @@ def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
     return 0
 
 
+def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
+    """Per-kernel durations of the headline's GPU work, from a rocprofv3 --kernel-trace file of
+    `bench.py --warmup W --steps K` (same W and K): the K timed forward+backward steps and the K
+    kernel-level steps (whose average step-2 duration is `kernels_us.bwd_main`), and the first
+    K steps from idle. Configs 3-5 run the same kernel names, so the dispatches are split into
+    steps (a step starts at a forward launch) and config 2's steps picked by the forward's name
+    and grid; the headline's are those after the last step of another config."""
+    rows = []
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            if "fattn::" not in r["Kernel_Name"]:
+                continue
+            name = r["Kernel_Name"].split("fattn::(anonymous namespace)::", 1)[-1]
+            name = name.split("(", 1)[0].replace("void ", "")
+            wgs = int(r["Grid_Size_X"]) // max(int(r["Workgroup_Size_X"]), 1)
+            rows.append((int(r["Start_Timestamp"]), name, wgs,
+                         (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    rows.sort()
+    b, h, s = CONFIGS[2][2], CONFIGS[2][3], CONFIGS[2][4]
+    main_fwd = (KERNEL_NAMES["fwd"], ((s + 127) // 128) * b * h)
+    steps_seq: list[list] = []
+    for t, name, wgs, us in rows:
+        if name.startswith("fwd_kernel") or not steps_seq:
+            steps_seq.append([])
+        steps_seq[-1].append((name, wgs, us))
+    is_main = [st[0][0] == main_fwd[0] and st[0][1] == main_fwd[1] for st in steps_seq]
+    other = [i for i, m in enumerate(is_main) if not m]
+    if other:
+        first = other[-1] + 1
+        idle = steps_seq[warmup:warmup + steps] if all(is_main[:warmup + steps]) else []
+    else:
+        first, idle = warmup + steps, steps_seq[warmup:warmup + steps]
+    timed = steps_seq[first + warmup:first + warmup + steps]
+    kern = steps_seq[first + warmup + 2 * steps:first + warmup + 3 * steps]
+    if len(timed) < steps or len(kern) < steps:
+        print(f"bench.py: the trace holds {len(steps_seq) - first} config-2 steps after the "
+              f"other configs; expected at least {warmup + 3 * steps}", file=sys.stderr)
+        return 1
+
+    def table(title, seq):
+        per: dict[str, list[float]] = {}
+        for st in seq:
+            for name, _, us in st:
+                per.setdefault(name, []).append(us)
+        total = sum(sum(v) for v in per.values())
+        print(f"\n{title}\n")
+        print("| kernel | calls | average (us) | median (us) | min (us) | max (us) | share |")
+        print("|---|--:|--:|--:|--:|--:|--:|")
+        for name, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            print(f"| `{name}` | {len(v)} | {statistics.mean(v):.1f} | {statistics.median(v):.1f} "
+                  f"| {min(v):.1f} | {max(v):.1f} | {100 * sum(v) / total:.1f} % |")
+
+    table(f"The {steps} timed forward+backward steps (after {warmup} warm-up steps)", timed)
+    table(f"The {steps} kernel-level steps (`kernels_us`, `roofline.achieved`)", kern)
+    if idle:
+        table(f"The first {steps} steps from idle (after {warmup} warm-up steps; "
+              "`fwd_bwd_from_idle_ms`)", idle)
+    return 0
+
+
 def time_extra(torch, w: Workload, steps: int, warmup: int) -> dict:
     """Op-level forward and forward+backward ms, and each kernel's us, of one extra config."""
     for _ in range(warmup):
@@ -305,10 +373,9 @@ def main() -> int:
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # MI355X raises its clocks over the first ~20 ms of sustained work (a kernel trace shows the
-    # forward going from 71 to 58 us per call over that time); the default 200 warm-up steps
-    # (~45 ms) put the timed steps at the steady state a training loop runs at. The line reports
-    # the first and last five timed steps, so a run with fewer warm-ups shows its ramp.
+    # MI355X raises its clocks over the first tens of milliseconds of sustained work (a kernel
+    # trace shows the forward going from 71 to 58 us per call) and lowers them within a second of
+    # idling. The line reports the first and last five timed steps, so a ramp shows.
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--causal", action="store_true", help="config 3 as the main workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -321,9 +388,15 @@ def main() -> int:
                          "to scale rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/traffic.json from two counter files and exit (no GPU)")
+    ap.add_argument("--trace-from", metavar="KERNEL_TRACE_CSV",
+                    help="print per-kernel durations of the headline's steps from a rocprofv3 "
+                         "kernel trace of this command with the same --warmup / --steps, and "
+                         "exit (no GPU)")
     args = ap.parse_args()
     if args.traffic_from:
         return summarize_traffic(*args.traffic_from)
+    if args.trace_from:
+        return summarize_trace(args.trace_from, max(args.warmup, 1), max(args.steps, 1))
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
               "(the op shards over (batch, head) with no communication; see DESIGN.md)",
@@ -354,6 +427,35 @@ def main() -> int:
         del src, dst
     log(f"bench: config {main_cfg} b{B} h{H} s{S} d{D}; warmup {args.warmup}, "
         f"steps {args.steps}")
+    K = max(args.steps, 1)
+    n5 = min(5, K)
+
+    # The same W + K steps from an idle GPU first ("cold"): MI355X lowers its clocks within a
+    # second of idling and raises them again over some tens of milliseconds of sustained work, so
+    # a short run started from idle measures the ramp. Then configs 3-5 are timed (about a second
+    # of sustained work), and the headline's W warm-up and K timed steps follow them directly, at
+    # the clocks a training loop runs at.
+    for _ in range(max(args.warmup, 1)):
+        w.step()
+    torch.cuda.synchronize()
+    cold_ms, cold_steps, _ = event_steps(torch, w.stream, w.step, K)
+    log(f"bench: from idle: fwd+bwd {cold_ms:.4f} ms (first {n5} steps "
+        f"{statistics.mean(cold_steps[:n5]):.4f}, last {n5} "
+        f"{statistics.mean(cold_steps[-n5:]):.4f})")
+
+    extra = {}
+    if not args.no_extra:
+        for cfg in (2, 3, 4, 5):
+            if cfg == main_cfg:
+                continue
+            xw = Workload(torch, L, _lib, dev, cfg)
+            # 100 warm-up steps: the first calls on a new shape touch freshly allocated pages,
+            # and config 3's steps (0.16 ms) would otherwise run while the clocks still rise.
+            extra[f"config{cfg}"] = time_extra(torch, xw, max(args.extra_steps, 1), 100)
+            log(f"bench: {CONFIGS[cfg][0]}: {json.dumps(extra[f'config{cfg}'])}")
+            del xw
+        torch.cuda.synchronize()
+
     for _ in range(max(args.warmup, 1)):
         w.step()
     torch.cuda.synchronize()
@@ -361,14 +463,12 @@ def main() -> int:
     # roctx ranges name the timed windows (the reference brackets them with cuProfilerStart /
     # Stop for an nsys capture range, examples/compare.rs:261-277); `rocprofv3 --marker-trace`
     # records them. torch.cuda.nvtx is roctx on ROCm.
-    K = max(args.steps, 1)
     torch.cuda.nvtx.range_push("fattn timed fwd+bwd")
     fwd_bwd_ms, per_step, fwd_bwd_wall = event_steps(torch, w.stream, w.step, K)
     torch.cuda.nvtx.range_pop()
     torch.cuda.nvtx.range_push("fattn timed fwd")
     fwd_ms, _, _ = event_steps(torch, w.stream, w.fwd, K)
     torch.cuda.nvtx.range_pop()
-    n5 = min(5, K)
     first5, last5 = statistics.mean(per_step[:n5]), statistics.mean(per_step[-n5:])
     log(f"bench: fwd+bwd {fwd_bwd_ms:.4f} ms (wall {fwd_bwd_wall:.4f}; first {n5} steps "
         f"{first5:.4f}, last {n5} {last5:.4f}), fwd {fwd_ms:.4f} ms")
@@ -417,6 +517,12 @@ def main() -> int:
         "fwd_bwd_wall_ms": round(fwd_bwd_wall, 5),
         "fwd_bwd_first5_ms": round(first5, 5),
         "fwd_bwd_last5_ms": round(last5, 5),
+        "fwd_bwd_from_idle_ms": round(cold_ms, 5),
+        "fwd_bwd_from_idle_first5_ms": round(statistics.mean(cold_steps[:n5]), 5),
+        "fwd_bwd_from_idle_last5_ms": round(statistics.mean(cold_steps[-n5:]), 5),
+        "sequence": ("W warm-up + K timed steps from idle (fwd_bwd_from_idle_ms), "
+                     + ("configs 3-5 timed (configs), " if extra else "")
+                     + "W warm-up + K timed steps (value), K forwards, K kernel-level steps"),
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_bwd_tflops": round(total_tflops, 3),
         "frac_fp32_peak": round(total_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
@@ -441,17 +547,7 @@ def main() -> int:
         },
     }
 
-    if not args.no_extra:
-        extra = {}
-        for cfg in (2, 3, 4, 5):
-            if cfg == main_cfg:
-                continue
-            xw = Workload(torch, L, _lib, dev, cfg)
-            # 25 warm-up steps: the first calls on a new shape touch freshly allocated pages.
-            extra[f"config{cfg}"] = time_extra(torch, xw, max(args.extra_steps, 1), 25)
-            log(f"bench: {CONFIGS[cfg][0]}: {json.dumps(extra[f'config{cfg}'])}")
-            del xw
-            torch.cuda.empty_cache()
+    if extra:
         result["configs"] = extra
 
     if not args.no_accuracy:
