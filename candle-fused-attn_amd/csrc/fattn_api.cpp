@@ -611,10 +611,13 @@ int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
 
 // Test hook (not declared in include/fattn.h; tests/test_boundary.py calls it without a GPU): an
 // audit of step 2's dQ-sum schedule for one shape, on the host, with the scheduling functions the
-// kernel runs (fattn_internal.h). out[0]: summing workgroups in step 2's grid; out[1]: those with a
-// (b, h) to sum; out[2]: violations -- a summing workgroup waits for a key block that runs on
-// another XCD, or xcd_remap and item_xcd disagree, or a workgroup past the plan's range has a
-// target; out[3]: query tiles two workgroups would both sum; out[4]: query tiles summed.
+// kernel runs (fattn_internal.h). A summing unit is a workgroup appended to step 2's grid
+// (non-causal) or a key block's own workgroup summing its diagonal tiles (causal). out[0]:
+// workgroups appended to step 2's grid; out[1]: summing units with tiles to sum; out[2]:
+// violations -- a unit waits for a key block that runs on another XCD or later in the grid, a
+// causal unit sums a tile it is not the last contributor of, xcd_remap and item_xcd disagree, or
+// a workgroup past the plan's range has a target; out[3]: query tiles two units would both sum;
+// out[4]: query tiles summed.
 int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int causal,
                              int64_t out[5]) {
   if (!out || b <= 0 || h <= 0 || s <= 0 || b * h * s > (int64_t{1} << 26)) return FATTN_EINVAL;
@@ -624,6 +627,7 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
   const int total = nkb * BH;
   const fattn::SumPlan plan = fattn::sum_plan(BH, nkb, ntile, static_cast<int>(d), causal);
   const int64_t nsum = fattn::bwd_sum_blocks(b, h, s, static_cast<int>(d), causal);
+  const bool sums = fattn::bwd_step2_sums(b, h, s, static_cast<int>(d), causal);
   int64_t targets = 0, bad = 0, twice = 0, covered = 0;
   // xcd_remap is a permutation and item_xcd its inverse's XCD.
   std::vector<char> seen(static_cast<size_t>(total), 0);
@@ -633,30 +637,55 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
       ++bad;
     }
   }
+  // The key blocks a unit summing tiles j0 .. j1 - 1 waits for: all, or (causal) those holding a
+  // key <= its last query.
+  auto need_of = [&](int j1) {
+    return causal ? static_cast<int>(std::min<int64_t>(nkb - 1, std::min<int64_t>(s - 1,
+                        int64_t{j1} * fattn::kBwdQueryTile - 1) / fattn::kBwdKeys)) + 1
+                  : nkb;
+  };
   std::vector<char> tile_done(static_cast<size_t>(BH) * ntile, 0);
-  for (int64_t i = 0; i < nsum + 64; ++i) {  // 64 past the grid: nothing may be assigned there
-    const int x = static_cast<int>(i & 7), m = static_cast<int>(i >> 3);
-    int bh = -1, j0 = -1;
-    if (!fattn::sum_target(plan, x, m, BH, causal, &bh, &j0)) continue;
-    if (i >= nsum || bh < 0 || bh >= BH || j0 < 0 || j0 >= ntile) {
-      ++bad;
-      continue;
-    }
-    ++targets;
-    const int j1 = std::min(ntile, j0 + fattn::kSumTiles);
-    // The key blocks the chunk waits for: all, or (causal) those holding a key <= its last query.
-    const int need = causal ? std::min<int64_t>(nkb - 1, std::min<int64_t>(s - 1,
-                                  int64_t{j1} * fattn::kBwdQueryTile - 1) / fattn::kBwdKeys) + 1
-                            : nkb;
-    for (int kb = 0; kb < need; ++kb) {
-      // Workgroup of key block kb of (b, h) bh: causal kb b h + bh (no remap); else the
-      // (b, h)-major item bh nkb + kb under xcd_remap.
-      const int xcd = causal ? ((kb * BH + bh) & 7) : fattn::item_xcd(bh * nkb + kb, total);
-      if (xcd != x) ++bad;
-    }
+  auto mark = [&](int bh, int j0, int j1) {
     for (int j = j0; j < j1; ++j) {
       if (tile_done[static_cast<size_t>(bh) * ntile + j]++) ++twice;
       ++covered;
+    }
+  };
+  if (causal) {
+    if (nsum != 0) ++bad;
+    // Key block kb of (b, h) bh is workgroup kb b h + bh (no remap).
+    for (int bh = 0; sums && bh < BH; ++bh) {
+      for (int kb = 0; kb < nkb; ++kb) {
+        int j0 = 0, j1 = 0;
+        fattn::own_tiles(kb, ntile, &j0, &j1);
+        if (j0 >= j1) continue;
+        ++targets;
+        const int id = kb * BH + bh, need = need_of(j1);
+        if (need != kb + 1 || need_of(j0 + 1) != kb + 1) ++bad;  // not its last contributor
+        for (int k = 0; k < need; ++k) {
+          const int idk = k * BH + bh;
+          if (idk > id || (idk & 7) != (id & 7)) ++bad;
+        }
+        mark(bh, j0, j1);
+      }
+    }
+  } else {
+    for (int64_t i = 0; i < nsum + 64; ++i) {  // 64 past the grid: nothing may be assigned there
+      const int x = static_cast<int>(i & 7), m = static_cast<int>(i >> 3);
+      int bh = -1, j0 = -1;
+      if (!fattn::sum_target(plan, x, m, BH, causal, &bh, &j0)) continue;
+      if (i >= nsum || bh < 0 || bh >= BH || j0 < 0 || j0 >= ntile) {
+        ++bad;
+        continue;
+      }
+      ++targets;
+      const int j1 = std::min(ntile, j0 + fattn::kSumTiles);
+      // Key block kb of (b, h) bh: the (b, h)-major item bh nkb + kb under xcd_remap; summing
+      // workgroups come after every key block in the grid.
+      for (int kb = 0; kb < need_of(j1); ++kb) {
+        if (fattn::item_xcd(bh * nkb + kb, total) != x) ++bad;
+      }
+      mark(bh, j0, j1);
     }
   }
   out[0] = nsum;

@@ -48,15 +48,23 @@ struct Workspace {
 Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d);
 constexpr int kCtrlTicket = 0;
 constexpr int kCtrlGuard = 32;
-// dQ sums inside step 2 (split mode, d <= 64): workgroups appended to step 2's grid sum query
-// tiles once every key block the tiles need has finished, if all of them ran on
-// the XCD the summing workgroup runs on (their partials are then in that XCD's L2 or written back
-// from it, so it reads them coherently); step 3 sums the rest. Every step 2 launch carries its own epoch (a 64-bit value unique to the launch, low 3
+// dQ sums inside step 2 (split mode, d <= 64): a query tile is summed in step 2 once every key
+// block it needs has finished, if all of them ran on the XCD of the workgroup that sums it (their
+// partials are then in that XCD's L2 or written back from it, so it reads them coherently); step
+// 3 sums the rest. Non-causal, workgroups appended to step 2's grid do the sums; causal, each key
+// block's own workgroup sums, after its walk, the tiles whose last contributor it is. Every step 2 launch carries its own epoch (a 64-bit value unique to the launch, low 3
 // bits zero): the key blocks' arrivals and the done flags hold it, so nothing needs clearing
 // between launches and no stale or uninitialised value passes for a current one (but with a
 // 2^-64 chance). The summing workgroups poll at most kSumMaxBlocks arrival slots.
 constexpr int kSumMaxBlocks = 256;
 constexpr int kSumTiles = 3;  // query tiles per summing workgroup
+// Causal: the query tiles whose last contributor is key block kb (its diagonal tiles; kBwdKeys /
+// kBwdQueryTile of them, fewer at the end of the sequence).
+constexpr int kOwnTiles = kBwdKeys / kBwdQueryTile;
+__host__ __device__ inline void own_tiles(int kb, int ntile, int* j0, int* j1) {
+  *j0 = kb * kOwnTiles;
+  *j1 = *j0 + kOwnTiles < ntile ? *j0 + kOwnTiles : ntile;
+}
 
 // Workgroups are dealt to the 8 XCDs round-robin (workgroup id % 8). xcd_remap gives each XCD a
 // contiguous range of logical items, so logical neighbours (the key blocks of one (b, h)) share
@@ -73,10 +81,10 @@ __host__ __device__ inline int item_xcd(int item, int total) {
   return item >= full ? (item & 7) : item / (full >> 3);
 }
 
-// The dQ sums in step 2's tail. `per` (b, h)s per XCD have every key block on that XCD: non-causal,
-// the (b, h)-major key blocks under xcd_remap, when F is a whole number of (b, h)s; causal, key
-// block kb of (b, h) is workgroup kb b h + bh, on XCD bh mod 8, when 8 divides b h. per = 0: no
-// sums (step 3 sums every tile). nchunk = chunks of kSumTiles query tiles per (b, h).
+// The dQ sums in step 2. `per` (b, h)s per XCD have every key block on that XCD: non-causal, the
+// (b, h)-major key blocks under xcd_remap, when F is a whole number of (b, h)s; causal, key block
+// kb of (b, h) is workgroup kb b h + bh, on XCD bh mod 8, when 8 divides b h. per = 0: no sums
+// (step 3 sums every tile). nchunk = chunks of kSumTiles query tiles per (b, h) (non-causal).
 struct SumPlan {
   int per, nchunk;
 };
@@ -91,18 +99,19 @@ __host__ __device__ inline SumPlan sum_plan(int BH, int nkb, int ntile, int d, i
   }
   return p;
 }
-// Summing workgroup m of XCD x (workgroup n_main + 8 m + x): the (b, h) it sums and its first
-// query tile. Non-causal: XCD x's (b, h)s one after the other; causal: tile-major (a tile's
-// contributors are the key blocks up to its last query, so the first tiles are complete first).
-// False for a workgroup with nothing to sum (m past the plan; never a (b, h) >= BH).
+// Non-causal summing workgroup m of XCD x (workgroup n_main + 8 m + x): the (b, h) it sums (XCD
+// x's (b, h)s one after the other) and its first query tile. False for a workgroup with nothing
+// to sum (m past the plan; never a (b, h) >= BH), and always when causal (no summing workgroups).
 __host__ __device__ inline bool sum_target(SumPlan p, int x, int m, int BH, int causal, int* bh,
                                            int* j0) {
-  if (p.per <= 0 || m >= p.per * p.nchunk) return false;
-  *bh = causal ? x + 8 * (m % p.per) : x * p.per + m / p.nchunk;
-  *j0 = (causal ? m / p.per : m % p.nchunk) * kSumTiles;
+  if (causal || p.per <= 0 || m >= p.per * p.nchunk) return false;
+  *bh = x * p.per + m / p.nchunk;
+  *j0 = m % p.nchunk * kSumTiles;
   return *bh < BH;
 }
-// Workgroups appended to step 2's grid for these sums (0: step 3 sums every tile).
+// Whether step 2 sums dQ tiles for this shape (the plan has (b, h)s to sum and the sums are on).
+bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal);
+// Workgroups appended to step 2's grid for the non-causal sums (0 when causal or without sums).
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal);
 // Step 2's sums on (the default) or off for every later backward of the process, so that a test
 // can compare both; returns the previous setting.

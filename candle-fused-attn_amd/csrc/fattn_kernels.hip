@@ -1256,35 +1256,40 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // folds such offsets into the LDS instructions, where across separate arrays it keeps an address
 // register per array (at D 64 that saves 24 registers).
 // ---------------------------------------------------------------------------------------------
-// dQ sums inside step 2 (split, D <= 64). Step 3 moves 118 MB at config 2 after step
-// 2's tail, where the CUs run fewer and fewer key blocks; workgroups appended to step 2's grid do
-// its sums in that tail instead. In-order dispatch starts them only once every key block has been
-// dispatched. Workgroup n_main + 8 m + x (on XCD x: workgroups go to the XCDs round robin on
-// MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks all run on XCD x
-// (sum_target: plan.per (b, h)s per XCD, kSumTiles tiles per chunk, in the order their key
-// blocks were dispatched; causal, a chunk waits only for the key blocks its tiles need; the host
-// sizes the grid from the same plan). Each key block, once its
-// partials are stored, writes the launch's epoch or'ed with its XCD to its arrival slot (agent
-// scope: written through to the coherence point, as the turn hand-over's counters). Wave 0 polls
-// the (b, h)'s slots (agent-scope loads) until every one holds this launch's epoch, sleeping
-// between polls, giving up after kSumPolls. The chunk is summed only if every key block ran on
-// this workgroup's XCD: all partials are then in this XCD's L2 (or written back from it). The sum
-// is step 3's, operation for operation: float4 i of a tile's partials in key-block order, times
-// scale (so the results are bit-identical whichever kernel sums a tile), stored from fragment
-// order straight into dQ rows (16 lanes write 64 contiguous bytes). Then the chunk's done flags
-// (the epoch); step 3 sums the tiles without one, so a key block on another XCD, or a poll that
-// gave up, only leaves work to step 3. Every poll ends: the key blocks have smaller workgroup
-// numbers on the same XCD, so they were dispatched before this workgroup and run to completion
-// whatever it does.
+// dQ sums inside step 2 (split, D <= 64). Step 3 moves 118 MB at config 2 after step 2's tail,
+// where the CUs run fewer and fewer key blocks; step 2 does those sums itself instead.
+// bwd_sum_range sums query tiles j0 .. j1 - 1 of one (b, h) once every key block they need has
+// finished. Each key block, once its partials are stored, writes the launch's epoch or'ed with its
+// XCD to its arrival slot (agent scope: written through to the coherence point, as the turn
+// hand-over's counters). Wave 0 polls the (b, h)'s slots (agent-scope loads) until every one it
+// needs holds this launch's epoch, sleeping between polls, giving up after kSumPolls. The tiles are
+// summed only if every key block ran on this workgroup's XCD: all partials are then in this XCD's
+// L2 (or written back from it). The sum is step 3's, operation for operation: float4 i of a tile's
+// partials in key-block order, times scale (so the results are bit-identical whichever kernel sums
+// a tile), stored from fragment order straight into dQ rows (16 lanes write 64 contiguous bytes).
+// Then the tiles' done flags (the epoch); step 3 sums the tiles without one, so a key block on
+// another XCD, or a poll that gave up, only leaves work to step 3.
+// Who sums:
+//   non-causal: workgroups appended to step 2's grid (in-order dispatch starts them only once every
+//   key block has been dispatched). Workgroup n_main + 8 m + x (on XCD x: workgroups go to the
+//   XCDs round robin on MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks all
+//   run on XCD x (sum_target: plan.per (b, h)s per XCD, kSumTiles tiles per chunk, in the order
+//   their key blocks were dispatched; the host sizes the grid from the same plan);
+//   causal: key block kb's own workgroup, after its walk, sums the tiles whose last contributor it
+//   is (own_tiles: its diagonal tiles 4 kb .. 4 kb + 3), which need key blocks 0 .. kb. Their
+//   workgroups kb' b h + bh come earlier in the grid and run on the same XCD (8 divides b h). No
+//   workgroup is appended: a tile is summed as soon as its last key block finishes, while other
+//   key blocks still run, where summing workgroups would start only after the last key block.
+//   At config 4 that is step 2 1202 -> 1116 us, at config 3 97.1 -> 93.6 us.
+// Every poll ends: the key blocks waited for have smaller workgroup numbers on the same XCD, so
+// they were dispatched before the polling workgroup and run to completion whatever it does.
 // kSumTiles query tiles per summing workgroup: at config 2, 1, 2 or 15 were slower and 4 the same.
 constexpr int kSumPolls = 4096;
-template <int D>
-__device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, unsigned* flag) {
+template <int D, int NT>
+__device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, int j1,
+                                              unsigned* flag) {
   constexpr int kDT = D / 16, kF4 = kQT * D / 4;
   const int tid = threadIdx.x, BH = a.B * a.H, ntile = a.ntile, nkb = a.nkb;
-  int bh, j0;
-  if (!sum_target(a.plan, x, m, BH, a.causal, &bh, &j0)) return;
-  const int j1 = min(ntile, j0 + kSumTiles);
   // Key blocks whose partials the chunk needs: all, or (causal) those holding a key <= its last
   // query.
   const int need = a.causal ? min(nkb - 1, min(a.S - 1, j1 * kQT - 1) / kBwdKeys) + 1 : nkb;
@@ -1317,16 +1322,16 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
   const int64_t row_stride = static_cast<int64_t>(3) * a.H * D;
   float* const dq_bh =
       a.dqkv + static_cast<int64_t>(b) * S * row_stride + static_cast<int64_t>(h) * D;
-  // Thread i sums float4 i of each of the chunk's tiles, four key blocks at a time: the loads of
-  // all the chunk's tiles for those key blocks are issued together, then added in key-block order.
+  // Thread i sums float4 i of each of the tiles, four key blocks at a time: the loads of all the
+  // tiles for those key blocks are issued together, then added in key-block order.
   static_assert(kF4 <= kThreads, "one float4 of each tile per thread");
   const int i = tid;
   if (i < kF4) {
-    int cnt[kSumTiles];
-    const float* src[kSumTiles];
-    f4 acc[kSumTiles];
+    int cnt[NT];
+    const float* src[NT];
+    f4 acc[NT];
 #pragma unroll
-    for (int jj = 0; jj < kSumTiles; ++jj) {
+    for (int jj = 0; jj < NT; ++jj) {
       const int j = min(j0 + jj, j1 - 1);
       cnt[jj] = j0 + jj >= j1 ? 0
                 : a.causal ? min(nkb - 1, min(S - 1, j * kQT + kQT - 1) / kBwdKeys) + 1
@@ -1334,9 +1339,9 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
       src[jj] = a.part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D) + 4 * i;
     }
     for (int kb0 = 0; kb0 < need; kb0 += 4) {
-      f4 x[kSumTiles][4];
+      f4 x[NT][4];
 #pragma unroll
-      for (int jj = 0; jj < kSumTiles; ++jj) {
+      for (int jj = 0; jj < NT; ++jj) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int kb = kb0 + k;
@@ -1344,7 +1349,7 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
         }
       }
 #pragma unroll
-      for (int jj = 0; jj < kSumTiles; ++jj) {
+      for (int jj = 0; jj < NT; ++jj) {
         if (kb0 < cnt[jj]) acc[jj] = kb0 == 0 ? x[jj][0] : acc[jj] + x[jj][0];
 #pragma unroll
         for (int k = 1; k < 4; ++k) {
@@ -1356,7 +1361,7 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
     const int lane = i & 63, md = i >> 6, dt = md % kDT, mm = md / kDT;
     const int lo = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int jj = 0; jj < kSumTiles; ++jj) {
+    for (int jj = 0; jj < NT; ++jj) {
       if (j0 + jj >= j1) break;
       const f4 r4 = acc[jj] * a.scale;
 #pragma unroll
@@ -1367,6 +1372,14 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
     }
   }
   if (tid < j1 - j0) a.done[static_cast<int64_t>(bh) * ntile + j0 + tid] = a.epoch;
+}
+
+// A non-causal summing workgroup (m of XCD x).
+template <int D>
+__device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, unsigned* flag) {
+  int bh, j0;
+  if (!sum_target(a.plan, x, m, a.B * a.H, a.causal, &bh, &j0)) return;
+  bwd_sum_range<D, kSumTiles>(a, bh, j0, min(a.ntile, j0 + kSumTiles), flag);
 }
 
 template <int D>
@@ -1642,6 +1655,12 @@ bwd_split_kernel(BwdArgs a) {
       st4(row + 2 * part + 16 * mt + 4 * g, dva[mt]);
     }
   }
+  if (a.causal && a.arrive != nullptr) {
+    // The tiles whose last contributor is this key block (the summing workgroups' work, causal).
+    int j0, j1;
+    own_tiles(kb, a.ntile, &j0, &j1);
+    bwd_sum_range<D, kOwnTiles>(a, bh, j0, j1, &sm.flag);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1820,9 +1839,15 @@ std::atomic<int> g_step2_sums{1};
 }  // namespace
 bool set_step2_sums(bool on) { return g_step2_sums.exchange(on ? 1 : 0) != 0; }
 
-int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
-  if (g_step2_sums.load(std::memory_order_relaxed) == 0) return 0;
+bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  if (g_step2_sums.load(std::memory_order_relaxed) == 0) return false;
   // The range check keeps b h s (hence every count below) inside int32.
+  const int nkb = static_cast<int>((s + kBwdKeys - 1) / kBwdKeys);
+  const int ntile = static_cast<int>((s + kQT - 1) / kQT);
+  return sum_plan(static_cast<int>(b * h), nkb, ntile, d, causal).per > 0;
+}
+int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  if (causal || !bwd_step2_sums(b, h, s, d, causal)) return 0;
   const int nkb = static_cast<int>((s + kBwdKeys - 1) / kBwdKeys);
   const int ntile = static_cast<int>((s + kQT - 1) / kQT);
   const SumPlan p = sum_plan(static_cast<int>(b * h), nkb, ntile, d, causal);
@@ -1830,7 +1855,7 @@ int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
 }
 int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal) {
   const int64_t tiles = bwd_dq_blocks(b, h, s);
-  if (bwd_sum_blocks(b, h, s, d, causal) == 0) return tiles;
+  if (!bwd_step2_sums(b, h, s, d, causal)) return tiles;
   const int64_t g = std::max<int64_t>(256, (tiles + kThreads - 1) / kThreads);
   return std::min(tiles, g);
 }
@@ -1868,7 +1893,9 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   const int stagger = !split && !causal && nkb <= kStaggerMaxBlocks ? 1 : 0;
   const int64_t nsum = split ? bwd_sum_blocks(b, h, s, d, causal) : 0;
   const int64_t nmain = (bwd_main_blocks(b, h, s) + 7) & ~int64_t{7};
-  if (nsum == 0) arrive = nullptr, done = nullptr, epoch_slot = nullptr;
+  if (!split || !bwd_step2_sums(b, h, s, d, causal)) {
+    arrive = nullptr, done = nullptr, epoch_slot = nullptr;
+  }
   const SumPlan plan = sum_plan(b * h, nkb, ntile, d, causal);
   BwdArgs a{q,    k,     v,    d_o,  o,    lse,   dsum,       dqkv,  part,
             arrive, done, epoch_slot, epoch, static_cast<int>(nmain), plan, turn, ctrl, b, h, s,
@@ -1930,7 +1957,7 @@ int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long lon
                   const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
                   float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
-  if (bwd_sum_blocks(b, h, s, d, causal) == 0) {
+  if (!bwd_step2_sums(b, h, s, d, causal)) {
     done = nullptr, arrive = nullptr, epoch_slot = nullptr;
   }
   void* args[] = {&part,  &done, &arrive, &epoch_slot, &dqkv,  &b,

@@ -279,22 +279,28 @@ def expected_sum_bh(bh, s, causal):
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_step2_dq_sum_schedule(causal):
-    """Step 2's summing workgroups, over many shapes (the kernel's own scheduling functions, run
-    on the host): every key block a summing workgroup waits for runs on that workgroup's XCD, no
-    target lies past b h (the case a rounded-up per-XCD count once produced: nkb = 1, b h not a
-    multiple of 8, e.g. h 17 s 50), no tile is summed twice, and exactly the (b, h)s the schedule's
-    definition puts wholly on one XCD are summed, every one of their tiles."""
+    """Step 2's dQ sums, over many shapes (the kernel's own scheduling functions, run on the
+    host): every key block a summing unit waits for runs on that unit's XCD and earlier in the
+    grid, no target lies past b h (the case a rounded-up per-XCD count once produced: nkb = 1, b h
+    not a multiple of 8, e.g. h 17 s 50), no tile is summed twice, and exactly the (b, h)s the
+    schedule's definition puts wholly on one XCD are summed, every one of their tiles.
+    Non-causal, the units are workgroups appended to the grid, ceil(ntile / 3) per (b, h); causal,
+    every key block's own workgroup sums its diagonal tiles (none appended)."""
     n = 0
     for s in (1, 16, 50, 64, 65, 100, 128, 200, 240, 333, 1024, 2048):
         for bh in list(range(1, 41)) + [48, 64, 96, 192, 384]:
             for d in (32, 64, 128):
                 a = sum_audit(1, bh, s, d, causal)
-                ntile = -(-s // 16)
+                ntile, nkb = -(-s // 16), -(-s // 64)
                 want_bh = expected_sum_bh(bh, s, causal) if d <= 64 else 0
                 assert a["bad"] == 0 and a["twice"] == 0, (s, bh, d, a)
                 assert a["covered"] == want_bh * ntile, (s, bh, d, a, want_bh)
-                nchunk = -(-ntile // 3)
-                assert a["grid"] == want_bh * nchunk and a["targets"] == a["grid"], (s, bh, d, a)
+                if causal:
+                    assert a["grid"] == 0 and a["targets"] == want_bh * nkb, (s, bh, d, a)
+                else:
+                    nchunk = -(-ntile // 3)
+                    assert a["grid"] == want_bh * nchunk and a["targets"] == a["grid"], \
+                        (s, bh, d, a)
                 n += 1
     assert n > 1000
     # The advisor's case: b 1, h 17, s 50 (one key block per (b, h)): 16 heads summed in step 2.
