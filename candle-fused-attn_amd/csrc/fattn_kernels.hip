@@ -111,16 +111,24 @@ __device__ __forceinline__ float lane_sum(float x) {
   return x;
 }
 
+// max of two floats as one v_max_f32: fmaxf on values from a lane swap makes the compiler quiet
+// both inputs first (two more v_max per call, 8 per forward tile), which NaN-free scores do not
+// need.
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 // max over lanes lo, lo + 16, lo + 32, lo + 48 (every lane gets it), on the VALU: the gfx950 row
 // swaps pair row r of one operand with row r ^ 1 (16-lane rows), then half h with h ^ 1
 // (32-lane halves); with both operands x, the max of the two results is the max of each pair.
 __device__ __forceinline__ float max4_groups(float x) {
   const unsigned u = __float_as_uint(x);
   const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  x = vmax(__uint_as_float(p[0]), __uint_as_float(p[1]));
   const unsigned v = __float_as_uint(x);
   const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+  return vmax(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 
 // v_permlane16_swap / v_permlane32_swap on a pair of floats (16-lane rows: the first swaps odd
@@ -554,7 +562,7 @@ fwd_kernel(FwdArgs a) {
             for (int r = 0; r < 4; ++r) {
               const float p = exp2_hw(fmaf(s[n][mt][r], c2, -mc));
               s[n][mt][r] = p;
-              psum += p;
+              psum = mt == 0 && r == 0 ? p : psum + p;
             }
           }
         } else {
@@ -567,7 +575,7 @@ fwd_kernel(FwdArgs a) {
               const float x = s[n][mt][r];
               const float p = x == kNegInf ? 0.0f : exp2_hw(fmaf(x, c2, -mc));
               s[n][mt][r] = p;
-              psum += p;
+              psum = mt == 0 && r == 0 ? p : psum + p;
             }
           }
         }
