@@ -13,7 +13,8 @@
 //
 // Device memory of outputs, copies and the backward workspace is taken stream-ordered
 // (hipMallocAsync / hipFreeAsync on the caller's stream); every launch is asynchronous on that
-// stream. There is no CPU path: the operators run on the HIP device only.
+// stream, so that stream must outlive the tensors allocated on it (their storage is given back
+// on it). There is no CPU path: the operators run on the HIP device only.
 #ifndef CANDLE_FUSED_ATTN_HPP
 #define CANDLE_FUSED_ATTN_HPP
 

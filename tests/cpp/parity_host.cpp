@@ -411,6 +411,48 @@ void gradient_views_share_the_qkv_layout() {
          "the views' buffer differs from fused_attention_qkv's gradient");
 }
 
+// The strided gather behind contiguous(), to_host() and the copy fallbacks: every view of a
+// [2, 3, 5, 7] tensor (transposes, a narrowed and squeezed slice, an offset) comes back in
+// row-major order of its logical shape, as computed on the host.
+void strided_copies_match_the_host() {
+  const Dims shape{2, 3, 5, 7};
+  std::vector<float> x(2 * 3 * 5 * 7);
+  for (std::size_t i = 0; i < x.size(); ++i) x[i] = static_cast<float>(i);
+  const cfa::Tensor t = cfa::Tensor::from_host(x, shape, g_stream);
+  auto at = [&](std::size_t a, std::size_t b, std::size_t c, std::size_t d) {
+    return x[((a * 3 + b) * 5 + c) * 7 + d];
+  };
+  // transpose(1, 3): [2, 7, 5, 3]
+  std::vector<float> want;
+  for (std::size_t a = 0; a < 2; ++a)
+    for (std::size_t d = 0; d < 7; ++d)
+      for (std::size_t c = 0; c < 5; ++c)
+        for (std::size_t b = 0; b < 3; ++b) want.push_back(at(a, b, c, d));
+  const cfa::Tensor tt = t.transpose(1, 3);
+  expect(!tt.is_contiguous(), "a transposed view is strided");
+  expect(tt.to_host(g_stream) == want, "transpose(1, 3) gathered wrong");
+  // narrow(2, 1, 3).narrow(1, 2, 1).squeeze(1): [2, 3, 7] at an offset
+  want.clear();
+  for (std::size_t a = 0; a < 2; ++a)
+    for (std::size_t c = 1; c < 4; ++c)
+      for (std::size_t d = 0; d < 7; ++d) want.push_back(at(a, 2, c, d));
+  const cfa::Tensor sl = t.narrow(2, 1, 3).narrow(1, 2, 1).squeeze(1);
+  expect(sl.layout().start_offset == 2 * 35 + 7, "slice offset");
+  const cfa::Tensor c = sl.contiguous(g_stream);
+  expect(c.is_contiguous() && c.layout().start_offset == 0, "contiguous copy at offset 0");
+  expect(c.to_host(g_stream) == want, "narrowed slice gathered wrong");
+  // reshape of a strided view copies first; of a contiguous one it is a view
+  const cfa::Tensor r = tt.reshape({2, 105}, g_stream);
+  expect(r.storage() != t.storage(), "reshape of a strided view copies");
+  expect(t.reshape({6, 35}, g_stream).storage() == t.storage(), "reshape of a contiguous view");
+  want.clear();
+  for (std::size_t a = 0; a < 2; ++a)
+    for (std::size_t d = 0; d < 7; ++d)
+      for (std::size_t cc = 0; cc < 5; ++cc)
+        for (std::size_t b = 0; b < 3; ++b) want.push_back(at(a, b, cc, d));
+  expect(r.to_host(g_stream) == want, "reshape copy order");
+}
+
 // Errors the C ABI raises (with the reference's messages) and the layer's own.
 void gpu_errors() {
   const Inputs in = inputs(1, 8, 2, 48);
@@ -529,6 +571,7 @@ const Case kCases[] = {
     {"backward_is_deterministic", true, backward_is_deterministic},
     {"copy_fallbacks_match_aligned_operands", true, copy_fallbacks_match_aligned_operands},
     {"gradient_views_share_the_qkv_layout", true, gradient_views_share_the_qkv_layout},
+    {"strided_copies_match_the_host", true, strided_copies_match_the_host},
     {"gpu_errors", true, gpu_errors},
 };
 

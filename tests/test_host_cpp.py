@@ -5,7 +5,8 @@ tests/cpp/parity_host, which mirrors the reference's integration tests (tests/pa
 empty inputs (nothing allocated or launched); `--gpu` the parity cases on the device: both entry
 points against the fp32 oracle at the reference's band (5e-6 max-abs, tests/parity.rs:209-220),
 the merged-heads layout, backward twice over one node, eight bit-identical reruns, copy fallbacks
-equal to aligned operands bit for bit, and the C ABI's errors. The program is built by
+equal to aligned operands bit for bit, the strided gather against the host, and the C ABI's
+errors. The program is built by
 __graft_entry__.build(); a missing build is a failure, not a skip.
 """
 from __future__ import annotations
