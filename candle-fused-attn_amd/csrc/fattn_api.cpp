@@ -617,12 +617,13 @@ int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
 // violations -- a unit waits for a key block that runs on another XCD or later in the grid, a
 // causal unit sums a tile it is not the last contributor of, xcd_remap and item_xcd disagree, or
 // a workgroup past the plan's range has a target; out[3]: query tiles two units would both sum;
-// out[4]: query tiles summed.
+// out[4]: query tiles summed; out[5]: keys per key block (bwd_split_keys).
 int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int causal,
-                             int64_t out[5]) {
+                             int64_t out[6]) {
   if (!out || b <= 0 || h <= 0 || s <= 0 || b * h * s > (int64_t{1} << 26)) return FATTN_EINVAL;
   const int BH = static_cast<int>(b * h);
-  const int nkb = static_cast<int>((s + fattn::kBwdKeys - 1) / fattn::kBwdKeys);
+  const int keys = fattn::bwd_split_keys(b, h, s, static_cast<int>(d), causal);
+  const int nkb = static_cast<int>((s + keys - 1) / keys);
   const int ntile = static_cast<int>((s + fattn::kBwdQueryTile - 1) / fattn::kBwdQueryTile);
   const int total = nkb * BH;
   const fattn::SumPlan plan = fattn::sum_plan(BH, nkb, ntile, static_cast<int>(d), causal);
@@ -641,7 +642,7 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
   // key <= its last query.
   auto need_of = [&](int j1) {
     return causal ? static_cast<int>(std::min<int64_t>(nkb - 1, std::min<int64_t>(s - 1,
-                        int64_t{j1} * fattn::kBwdQueryTile - 1) / fattn::kBwdKeys)) + 1
+                        int64_t{j1} * fattn::kBwdQueryTile - 1) / keys)) + 1
                   : nkb;
   };
   std::vector<char> tile_done(static_cast<size_t>(BH) * ntile, 0);
@@ -657,7 +658,7 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
     for (int bh = 0; sums && bh < BH; ++bh) {
       for (int kb = 0; kb < nkb; ++kb) {
         int j0 = 0, j1 = 0;
-        fattn::own_tiles(kb, ntile, &j0, &j1);
+        fattn::own_tiles(kb, keys, ntile, &j0, &j1);
         if (j0 >= j1) continue;
         ++targets;
         const int id = kb * BH + bh, need = need_of(j1);
@@ -693,6 +694,7 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
   out[2] = bad;
   out[3] = twice;
   out[4] = covered;
+  out[5] = keys;
   return 0;
 }
 

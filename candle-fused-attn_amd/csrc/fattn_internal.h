@@ -58,12 +58,12 @@ constexpr int kCtrlGuard = 32;
 // 2^-64 chance). The summing workgroups poll at most kSumMaxBlocks arrival slots.
 constexpr int kSumMaxBlocks = 256;
 constexpr int kSumTiles = 3;  // query tiles per summing workgroup
-// Causal: the query tiles whose last contributor is key block kb (its diagonal tiles; kBwdKeys /
-// kBwdQueryTile of them, fewer at the end of the sequence).
-constexpr int kOwnTiles = kBwdKeys / kBwdQueryTile;
-__host__ __device__ inline void own_tiles(int kb, int ntile, int* j0, int* j1) {
-  *j0 = kb * kOwnTiles;
-  *j1 = *j0 + kOwnTiles < ntile ? *j0 + kOwnTiles : ntile;
+// Causal: the query tiles whose last contributor is key block kb of `keys` keys (its diagonal
+// tiles; keys / kBwdQueryTile of them, fewer at the end of the sequence).
+__host__ __device__ inline void own_tiles(int kb, int keys, int ntile, int* j0, int* j1) {
+  const int n = keys / kBwdQueryTile;
+  *j0 = kb * n;
+  *j1 = *j0 + n < ntile ? *j0 + n : ntile;
 }
 
 // Workgroups are dealt to the 8 XCDs round-robin (workgroup id % 8). xcd_remap gives each XCD a
@@ -109,6 +109,10 @@ __host__ __device__ inline bool sum_target(SumPlan p, int x, int m, int BH, int 
   *j0 = m % p.nchunk * kSumTiles;
   return *bh < BH;
 }
+// Keys per key block of the split step 2 (d <= 64): kBwdKeys, or twice that (each wave owning two
+// groups of 16 keys) for long non-causal sequences at d 64. The sums' plan, step 3 and the
+// workspace's slots (sized for kBwdKeys) follow it.
+int bwd_split_keys(int64_t b, int64_t h, int64_t s, int d, int causal);
 // Whether step 2 sums dQ tiles for this shape (the plan has (b, h)s to sum and the sums are on).
 bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal);
 // Workgroups appended to step 2's grid for the non-causal sums (0 when causal or without sums).

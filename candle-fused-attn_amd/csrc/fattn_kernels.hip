@@ -741,6 +741,7 @@ struct BwdArgs {
   float scale;
   int causal;
   int stagger;  // non-causal only: spread the key blocks' walks over the tiles (see below)
+  int kkeys;    // keys per key block (split: 64 KG)
 };
 
 // Staggered walks make a key block wait on blocks of its own (b, h) that hold later tickets; that
@@ -1300,7 +1301,7 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
   const int tid = threadIdx.x, BH = a.B * a.H, ntile = a.ntile, nkb = a.nkb;
   // Key blocks whose partials the chunk needs: all, or (causal) those holding a key <= its last
   // query.
-  const int need = a.causal ? min(nkb - 1, min(a.S - 1, j1 * kQT - 1) / kBwdKeys) + 1 : nkb;
+  const int need = a.causal ? min(nkb - 1, min(a.S - 1, j1 * kQT - 1) / a.kkeys) + 1 : nkb;
   if (tid < 64) {
     unsigned xcc;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
@@ -1342,7 +1343,7 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
     for (int jj = 0; jj < NT; ++jj) {
       const int j = min(j0 + jj, j1 - 1);
       cnt[jj] = j0 + jj >= j1 ? 0
-                : a.causal ? min(nkb - 1, min(S - 1, j * kQT + kQT - 1) / kBwdKeys) + 1
+                : a.causal ? min(nkb - 1, min(S - 1, j * kQT + kQT - 1) / a.kkeys) + 1
                            : nkb;
       src[jj] = a.part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D) + 4 * i;
     }
@@ -1390,9 +1391,10 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
   bwd_sum_range<D, kSumTiles>(a, bh, j0, min(a.ntile, j0 + kSumTiles), flag);
 }
 
-template <int D>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BWD_WAVES)))
+template <int D, int KG>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(KG == 1 ? BWD_WAVES : 2)))
 bwd_split_kernel(BwdArgs a) {
+  constexpr int kKeys = kBwdKeys * KG;
   static_assert(D <= 64, "D 128 has no LDS room for three buffers: bwd_kernel<true, 128>");
   static_assert(kNS == 1, "one 16-query subtile per tile");
   constexpr int kKR = D / 4;                  // K (or V) values per lane: B operands of S, dP
@@ -1402,7 +1404,7 @@ bwd_split_kernel(BwdArgs a) {
   typedef float Tile[kQT * D];
   struct Smem {
     Tile q[kNB], g[kNB], o[kNB];
-    float ds[kNB][kQT * kBwdKeys];
+    float ds[kNB][kQT * kKeys];
     float l[kNB][kQT], d[kNB][kQT];
     unsigned flag;  // a dQ sum's poll result, from thread 0 to the workgroup
   };
@@ -1437,9 +1439,9 @@ bwd_split_kernel(BwdArgs a) {
   const int bh = a.causal ? item % BH : item / a.nkb;
   const int kb = a.causal ? item / BH : item % a.nkb;
   const int b = bh / a.H, h = bh % a.H;
-  const int k0 = kb * kBwdKeys;
-  const int kw0 = k0 + 16 * w;  // the wave's first key
-  const int key = kw0 + lo;     // this lane's key
+  const int k0 = kb * kKeys;
+  const int kw0 = k0 + 16 * KG * w;  // the wave's first key (KG groups of 16)
+  const int key = kw0 + lo;          // this lane's key in group 0 (group c: + 16 c)
   const int t0 = a.causal ? k0 / kQT : 0;
   const int nsteps = a.ntile - t0;
 
@@ -1456,16 +1458,22 @@ bwd_split_kernel(BwdArgs a) {
   // K, V of this lane's key (B operands of S and dP) and kQ[t] = K[k0 + 16 g + t][16 w + lo]
   // (B operand of the dQ product), zero past S.
   // (Loads issued here; K and V are placed after the first tiles' copies are issued, below.)
-  float kB[kKR], vB[kKR], kQ[16];
-  Quarter<D> kload, vload;
+  float kB[KG][kKR], vB[KG][kKR], kQ[KG][16];
+  Quarter<D> kload[KG], vload[KG];
   {
-    const int kr = min(key, S - 1);
-    quarter_issue<D>(kp + kr * a.k.ss, g, kload);
-    quarter_issue<D>(vp + kr * a.v.ss, g, vload);
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int kk = k0 + 16 * g + t;
-      kQ[t] = kk < S && wave_dq ? kp[min(kk, S - 1) * a.k.ss + 16 * w + lo] : 0.0f;
+    for (int c = 0; c < KG; ++c) {
+      const int kr = min(key + 16 * c, S - 1);
+      quarter_issue<D>(kp + kr * a.k.ss, g, kload[c]);
+      quarter_issue<D>(vp + kr * a.v.ss, g, vload[c]);
+    }
+#pragma unroll
+    for (int hh = 0; hh < KG; ++hh) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int kk = k0 + 64 * hh + 16 * g + t;
+        kQ[hh][t] = kk < S && wave_dq ? kp[min(kk, S - 1) * a.k.ss + 16 * w + lo] : 0.0f;
+      }
     }
   }
 
@@ -1515,24 +1523,30 @@ bwd_split_kernel(BwdArgs a) {
   float* const slot = a.part + (static_cast<int64_t>(kb) * BH + bh) * a.ntile * (kQT * D) +
                       256 * w + 4 * lane;
 
-  f4 dva[kDT], dka[kDT];
+  f4 dva[KG][kDT], dka[KG][kDT];
 #pragma unroll
-  for (int mt = 0; mt < kDT; ++mt) {
-    dva[mt] = zero4();
-    dka[mt] = zero4();
+  for (int c = 0; c < KG; ++c) {
+#pragma unroll
+    for (int mt = 0; mt < kDT; ++mt) {
+      dva[c][mt] = zero4();
+      dka[c][mt] = zero4();
+    }
   }
   f4 p1 = zero4();  // the dQ fragment of the last tile (stored at the start of the next)
   auto store_frag = [&](int j) { st4(slot + j * (kQT * D), p1); };
 
   gload(0, Const<0>{});
   if (nsteps > 1) gload(1, Const<1>{});
-  quarter_place<D>(kload, kB);
-  quarter_place<D>(vload, vB);
-  if (kw0 + 16 > S) {  // wave-uniform: only a wave with keys past S zeroes them
 #pragma unroll
-    for (int t = 0; t < kKR; ++t) {
-      kB[t] = key < S ? kB[t] : 0.0f;
-      vB[t] = key < S ? vB[t] : 0.0f;
+  for (int c = 0; c < KG; ++c) {
+    quarter_place<D>(kload[c], kB[c]);
+    quarter_place<D>(vload[c], vB[c]);
+    if (kw0 + 16 * c + 16 > S) {  // wave-uniform: only a group with keys past S zeroes them
+#pragma unroll
+      for (int t = 0; t < kKR; ++t) {
+        kB[c][t] = key + 16 * c < S ? kB[c][t] : 0.0f;
+        vB[c][t] = key + 16 * c < S ? vB[c][t] : 0.0f;
+      }
     }
   }
   wait_mem();  // the direct copies have landed
@@ -1553,46 +1567,57 @@ bwd_split_kernel(BwdArgs a) {
     const float* Qt = sQ[buf];
     const float* Gt = sdO[buf];
 
-    // Wave-uniform liveness of this wave's 16 keys for the tile's 16 queries.
-    const bool live = q0 < S && kw0 < S && !(a.causal && kw0 > q0 + 15);
-
-    // S and dP.
-    f4 sS = zero4(), sP = zero4();
-    if (live) {
+    // Wave-uniform liveness of each group's 16 keys for the tile's 16 queries (a live group 1
+    // implies a live group 0).
+    bool live[KG];
+    f4 sS[KG], sP[KG];
+#pragma unroll
+    for (int c = 0; c < KG; ++c) {
+      const int kc = kw0 + 16 * c;
+      live[c] = q0 < S && kc < S && !(a.causal && kc > q0 + 15);
+      sS[c] = zero4();
+      sP[c] = zero4();
+    }
+    if (live[0]) {
 #pragma unroll
       for (int u = 0; u < kKR / 4; ++u) {
         const int at = swz<D>(lo, kKR * g + 4 * u);
         const f4 x = ld4(Qt + at), y = ld4(Gt + at);
-        sS = mma(x.x, kB[4 * u], sS);
-        sS = mma(x.y, kB[4 * u + 1], sS);
-        sS = mma(x.z, kB[4 * u + 2], sS);
-        sS = mma(x.w, kB[4 * u + 3], sS);
-        sP = mma(y.x, vB[4 * u], sP);
-        sP = mma(y.y, vB[4 * u + 1], sP);
-        sP = mma(y.z, vB[4 * u + 2], sP);
-        sP = mma(y.w, vB[4 * u + 3], sP);
+#pragma unroll
+        for (int c = 0; c < KG; ++c) {
+          if (!live[c]) continue;
+          sS[c] = mma(x.x, kB[c][4 * u], sS[c]);
+          sS[c] = mma(x.y, kB[c][4 * u + 1], sS[c]);
+          sS[c] = mma(x.z, kB[c][4 * u + 2], sS[c]);
+          sS[c] = mma(x.w, kB[c][4 * u + 3], sS[c]);
+          sP[c] = mma(y.x, vB[c][4 * u], sP[c]);
+          sP[c] = mma(y.y, vB[c][4 * u + 1], sP[c]);
+          sP[c] = mma(y.z, vB[c][4 * u + 2], sP[c]);
+          sP[c] = mma(y.w, vB[c][4 * u + 3], sP[c]);
+        }
       }
-
-      // P = exp(S scale - L), dS = P o (dP - D); lane (lo, g), register r: query q0 + 4 g + r,
-      // key `key`. Then dV^T and dK^T.
       const f4 Lv = ld4(&sL[buf][4 * g]), Dv = ld4(&sD[buf][4 * g]);
       const int qi0 = q0 + 4 * g;
-      if ((!a.causal || kw0 + 15 <= q0) && q0 + 16 <= S && kw0 + 16 <= S) {
-        // Every query and key live (causal: every key at or before every query): no mask.
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = exp2_hw(fmaf(sS[r], a.scale, -Lv[r]) * kLog2e);
-          sP[r] = p * (sP[r] - Dv[r]);  // dS
-          sS[r] = p;                     // P
-        }
-      } else {
+      for (int c = 0; c < KG; ++c) {
+        if (!live[c]) continue;
+        const int kc = kw0 + 16 * c, keyc = key + 16 * c;
+        if ((!a.causal || kc + 15 <= q0) && q0 + 16 <= S && kc + 16 <= S) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool ok = qi0 + r < S && key < S && !(a.causal && key > qi0 + r);
-          const float e = exp2_hw(fmaf(sS[r], a.scale, -Lv[r]) * kLog2e);
-          const float p = ok ? e : 0.0f;
-          sP[r] = p * (sP[r] - Dv[r]);  // dS
-          sS[r] = p;                     // P
+          for (int r = 0; r < 4; ++r) {
+            const float p = exp2_hw(fmaf(sS[c][r], a.scale, -Lv[r]) * kLog2e);
+            sP[c][r] = p * (sP[c][r] - Dv[r]);  // dS
+            sS[c][r] = p;                        // P
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const bool ok = qi0 + r < S && keyc < S && !(a.causal && keyc > qi0 + r);
+            const float e = exp2_hw(fmaf(sS[c][r], a.scale, -Lv[r]) * kLog2e);
+            const float p = ok ? e : 0.0f;
+            sP[c][r] = p * (sP[c][r] - Dv[r]);  // dS
+            sS[c][r] = p;                        // P
+          }
         }
       }
 #pragma unroll
@@ -1600,15 +1625,25 @@ bwd_split_kernel(BwdArgs a) {
 #pragma unroll
         for (int mt = 0; mt < kDT; ++mt) {
           const int at = swz<D>(4 * g + r, 16 * mt + lo);
-          dva[mt] = mma(Gt[at], sS[r], dva[mt]);
-          dka[mt] = mma(Qt[at], sP[r], dka[mt]);
+          const float gv = Gt[at], qv = Qt[at];
+#pragma unroll
+          for (int c = 0; c < KG; ++c) {
+            if (!live[c]) continue;
+            dva[c][mt] = mma(gv, sS[c][r], dva[c][mt]);
+            dka[c][mt] = mma(qv, sP[c][r], dka[c][mt]);
+          }
         }
       }
     }
 
-    // This tile's dS into LDS (zero where the wave's keys are all masked).
+    // This tile's dS into LDS (zero where a group's keys are all masked).
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sdS[buf][swz<kBwdKeys>(4 * g + r, 16 * w + lo)] = sP[r];
+    for (int c = 0; c < KG; ++c) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sdS[buf][swz<kKeys>(4 * g + r, 16 * (KG * w + c) + lo)] = sP[c][r];
+      }
+    }
     if (frag_pending) {
       wait_vm<1>();  // tile t + 2's copies complete (the fragment's store, issued after, need not)
     } else {
@@ -1620,12 +1655,15 @@ bwd_split_kernel(BwdArgs a) {
     p1 = zero4();
     if (q0 < S && wave_dq) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const f4 x = ld4(&sdS[buf][swz<kBwdKeys>(lo, 16 * g + 4 * u)]);
-        p1 = mma(x.x, kQ[4 * u], p1);
-        p1 = mma(x.y, kQ[4 * u + 1], p1);
-        p1 = mma(x.z, kQ[4 * u + 2], p1);
-        p1 = mma(x.w, kQ[4 * u + 3], p1);
+      for (int hh = 0; hh < KG; ++hh) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const f4 x = ld4(&sdS[buf][swz<kKeys>(lo, 64 * hh + 16 * g + 4 * u)]);
+          p1 = mma(x.x, kQ[hh][4 * u], p1);
+          p1 = mma(x.y, kQ[hh][4 * u + 1], p1);
+          p1 = mma(x.z, kQ[hh][4 * u + 2], p1);
+          p1 = mma(x.w, kQ[hh][4 * u + 3], p1);
+        }
       }
     }
     // D of tile t + 2 (its rows landed before the barrier).
@@ -1652,22 +1690,26 @@ bwd_split_kernel(BwdArgs a) {
     }
   }
 
-  // dK (x scale) and dV of this lane's key: dims 16 mt + 4 g .. + 3, one float4 each.
-  if (key < S) {
-    float* row = a.dqkv + (static_cast<int64_t>(b) * S + key) * 3 * a.H * D +
-                 static_cast<int64_t>(h) * D;
-    const int64_t part = static_cast<int64_t>(a.H) * D;
+  // dK (x scale) and dV of this lane's keys: dims 16 mt + 4 g .. + 3, one float4 each.
 #pragma unroll
-    for (int mt = 0; mt < kDT; ++mt) {
-      st4(row + part + 16 * mt + 4 * g, dka[mt] * a.scale);
-      st4(row + 2 * part + 16 * mt + 4 * g, dva[mt]);
+  for (int c = 0; c < KG; ++c) {
+    const int keyc = key + 16 * c;
+    if (keyc < S) {
+      float* row = a.dqkv + (static_cast<int64_t>(b) * S + keyc) * 3 * a.H * D +
+                   static_cast<int64_t>(h) * D;
+      const int64_t part = static_cast<int64_t>(a.H) * D;
+#pragma unroll
+      for (int mt = 0; mt < kDT; ++mt) {
+        st4(row + part + 16 * mt + 4 * g, dka[c][mt] * a.scale);
+        st4(row + 2 * part + 16 * mt + 4 * g, dva[c][mt]);
+      }
     }
   }
   if (a.causal && a.arrive != nullptr) {
     // The tiles whose last contributor is this key block (the summing workgroups' work, causal).
     int j0, j1;
-    own_tiles(kb, a.ntile, &j0, &j1);
-    bwd_sum_range<D, kOwnTiles>(a, bh, j0, j1, &sm.flag);
+    own_tiles(kb, kKeys, a.ntile, &j0, &j1);
+    bwd_sum_range<D, kKeys / kQT>(a, bh, j0, j1, &sm.flag);
   }
 }
 
@@ -1682,13 +1724,13 @@ bwd_split_kernel(BwdArgs a) {
 template <int D>
 __device__ __forceinline__ void dq_tile(const float* __restrict__ part, float* __restrict__ dqkv,
                                         int B, int H, int S, int nkb, int ntile, float scale,
-                                        int causal, int bh, int j, float* tile) {
+                                        int causal, int bh, int j, float* tile, int kkeys) {
   constexpr int kDT = D / 16, kPitch = D + 4;  // pitch: conflict-free fragment writes
   constexpr int kF4 = kQT * D / 4;             // float4s per tile
   const int tid = threadIdx.x;
   const int b = bh / H, h = bh % H, q0 = j * kQT;
   // Contributors: causal, the key blocks holding a key <= the tile's last query.
-  const int cnt = causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kBwdKeys) + 1 : nkb;
+  const int cnt = causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kkeys) + 1 : nkb;
   const int64_t slot = static_cast<int64_t>(B) * H * ntile * (kQT * D);
   const float* src = part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D);
 #pragma unroll
@@ -1736,7 +1778,7 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
                                                      const unsigned long long* __restrict__ epoch,
                                                      float* __restrict__ dqkv, int B, int H,
                                                      int S, int nkb, int ntile, float scale,
-                                                     int causal) {
+                                                     int causal, int kkeys) {
   __shared__ __attribute__((aligned(16))) float tile[kQT * (D + 4)];
   __shared__ int todo[kThreads];
   __shared__ int ntodo;
@@ -1747,7 +1789,8 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
     // still cached.
     int it = static_cast<int>(blockIdx.x);
     if (!causal && it < (tot & ~7)) it = (it & 7) * (tot >> 3) + ((tot >> 3) - 1 - (it >> 3));
-    dq_tile<D>(part, dqkv, B, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile, tile);
+    dq_tile<D>(part, dqkv, B, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile, tile,
+               kkeys);
     return;
   }
   const int tid = threadIdx.x;
@@ -1767,7 +1810,8 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
   const int k = ntodo;
   for (int i = 0; i < k; ++i) {
     const int it = todo[i];
-    dq_tile<D>(part, dqkv, B, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile, tile);
+    dq_tile<D>(part, dqkv, B, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile, tile,
+               kkeys);
     __syncthreads();  // the LDS tile is reused
   }
 }
@@ -1847,16 +1891,27 @@ std::atomic<int> g_step2_sums{1};
 }  // namespace
 bool set_step2_sums(bool on) { return g_step2_sums.exchange(on ? 1 : 0) != 0; }
 
+int bwd_split_keys(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  // 128-key blocks (two 16-key groups per wave, 2 waves per SIMD): half the dQ partials and half
+  // the per-tile staging and barriers per product, against one wave per SIMD fewer. Measured
+  // (step 2, non-causal, d 64): s 384 +3.9 %, 512 -4.8 %, 768 -4.1 %, 1024 -6.7 %, 2048 -6.9 %,
+  // 4096 -3.6 %; causal +1 to +31 % (the diagonal blocks' masked work doubles). They need two
+  // workgroups per CU to fill the chip.
+  if (d != 64 || causal || s < 512) return kBwdKeys;
+  return (s + 2 * kBwdKeys - 1) / (2 * kBwdKeys) * b * h >= 512 ? 2 * kBwdKeys : kBwdKeys;
+}
 bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal) {
   if (g_step2_sums.load(std::memory_order_relaxed) == 0) return false;
   // The range check keeps b h s (hence every count below) inside int32.
-  const int nkb = static_cast<int>((s + kBwdKeys - 1) / kBwdKeys);
+  const int keys = bwd_split_keys(b, h, s, d, causal);
+  const int nkb = static_cast<int>((s + keys - 1) / keys);
   const int ntile = static_cast<int>((s + kQT - 1) / kQT);
   return sum_plan(static_cast<int>(b * h), nkb, ntile, d, causal).per > 0;
 }
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
   if (causal || !bwd_step2_sums(b, h, s, d, causal)) return 0;
-  const int nkb = static_cast<int>((s + kBwdKeys - 1) / kBwdKeys);
+  const int keys = bwd_split_keys(b, h, s, d, causal);
+  const int nkb = static_cast<int>((s + keys - 1) / keys);
   const int ntile = static_cast<int>((s + kQT - 1) / kQT);
   const SumPlan p = sum_plan(static_cast<int>(b * h), nkb, ntile, d, causal);
   return int64_t{8} * p.per * p.nchunk;
@@ -1898,22 +1953,25 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
                     float scale, int causal, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
   const bool split = part != nullptr;
+  const int kkeys = split && d <= 64 ? bwd_split_keys(b, h, s, d, causal) : kBwdKeys;
+  nkb = (s + kkeys - 1) / kkeys;
   const int stagger = !split && !causal && nkb <= kStaggerMaxBlocks ? 1 : 0;
   const int64_t nsum = split ? bwd_sum_blocks(b, h, s, d, causal) : 0;
-  const int64_t nmain = (bwd_main_blocks(b, h, s) + 7) & ~int64_t{7};
+  const int64_t nblk = int64_t{nkb} * b * h;
+  const int64_t nmain = (nblk + 7) & ~int64_t{7};
   if (!split || !bwd_step2_sums(b, h, s, d, causal)) {
     arrive = nullptr, done = nullptr, epoch_slot = nullptr;
   }
   const SumPlan plan = sum_plan(b * h, nkb, ntile, d, causal);
   BwdArgs a{q,    k,     v,    d_o,  o,    lse,   dsum,       dqkv,  part,
             arrive, done, epoch_slot, epoch, static_cast<int>(nmain), plan, turn, ctrl, b, h, s,
-            nkb,  ntile, scale, causal, stagger};
+            nkb,  ntile, scale, causal, stagger, kkeys};
   void* args[] = {&a};
   if (split && d <= 64) {
-    const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32>)
-                             : reinterpret_cast<const void*>(bwd_split_kernel<64>);
-    return static_cast<int>(
-        launch(fn, nsum ? nmain + nsum : bwd_main_blocks(b, h, s), args, stream));
+    const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32, 1>)
+                     : kkeys == kBwdKeys ? reinterpret_cast<const void*>(bwd_split_kernel<64, 1>)
+                                         : reinterpret_cast<const void*>(bwd_split_kernel<64, 2>);
+    return static_cast<int>(launch(fn, nsum ? nmain + nsum : nblk, args, stream));
   }
   // The turn mode at every head_dim; the split mode at 128 (no LDS room for bwd_split_kernel).
   const void* fn;
@@ -1964,12 +2022,13 @@ int static_scratch(void* stream, void** out) {
 int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long long* arrive,
                   const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
                   float scale, int causal, void* stream) {
-  int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
+  int kkeys = bwd_split_keys(b, h, s, d, causal);
+  int nkb = (s + kkeys - 1) / kkeys, ntile = (s + kQT - 1) / kQT;
   if (!bwd_step2_sums(b, h, s, d, causal)) {
     done = nullptr, arrive = nullptr, epoch_slot = nullptr;
   }
   void* args[] = {&part,  &done, &arrive, &epoch_slot, &dqkv,  &b,
-                  &h,     &s,    &nkb,    &ntile,      &scale, &causal};
+                  &h,     &s,    &nkb,    &ntile,      &scale, &causal, &kkeys};
   const void* fn = d == 32    ? reinterpret_cast<const void*>(dq_kernel<32>)
                    : d == 128 ? reinterpret_cast<const void*>(dq_kernel<128>)
                               : reinterpret_cast<const void*>(dq_kernel<64>);

@@ -258,17 +258,26 @@ def sum_audit(b, h, s, d, causal):
     f = L.fattn_internal_sum_audit
     f.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.POINTER(ctypes.c_int64)]
     f.restype = ctypes.c_int
-    out = (ctypes.c_int64 * 5)()
+    out = (ctypes.c_int64 * 6)()
     assert f(b, h, s, d, int(causal), out) == 0
-    return dict(zip(("grid", "targets", "bad", "twice", "covered"), list(out)))
+    return dict(zip(("grid", "targets", "bad", "twice", "covered", "keys"), list(out)))
 
 
-def expected_sum_bh(bh, s, causal):
+def expected_keys(bh, s, d, causal):
+    """Keys per split key block, from the rule's definition: 128 (two 16-key groups per wave) for
+    non-causal d 64 from s 512 on when ceil(s / 128) b h >= 512 workgroups fill two per CU; else
+    64."""
+    if d == 64 and not causal and s >= 512 and -(-s // 128) * bh >= 512:
+        return 128
+    return 64
+
+
+def expected_sum_bh(bh, s, causal, keys=64):
     """Restated from the schedule's definition: the (b, h)s whose key blocks all run on one XCD
     when workgroups go to the 8 XCDs round-robin. Non-causal: (b, h)-major key blocks under
     xcd_remap, XCD x holding items [x F, (x + 1) F), F = floor(nkb b h / 8) -- a whole number of
     (b, h)s per XCD or no sums; causal: 8 must divide b h."""
-    nkb = -(-s // 64)
+    nkb = -(-s // keys)
     if nkb > 256:
         return 0
     if causal:
@@ -287,12 +296,14 @@ def test_step2_dq_sum_schedule(causal):
     Non-causal, the units are workgroups appended to the grid, ceil(ntile / 3) per (b, h); causal,
     every key block's own workgroup sums its diagonal tiles (none appended)."""
     n = 0
-    for s in (1, 16, 50, 64, 65, 100, 128, 200, 240, 333, 1024, 2048):
-        for bh in list(range(1, 41)) + [48, 64, 96, 192, 384]:
+    for s in (1, 16, 50, 64, 65, 100, 128, 200, 240, 333, 511, 512, 600, 1024, 2048):
+        for bh in list(range(1, 41)) + [48, 64, 96, 128, 192, 256, 384]:
             for d in (32, 64, 128):
                 a = sum_audit(1, bh, s, d, causal)
-                ntile, nkb = -(-s // 16), -(-s // 64)
-                want_bh = expected_sum_bh(bh, s, causal) if d <= 64 else 0
+                keys = expected_keys(bh, s, d, causal)
+                assert a["keys"] == keys, (s, bh, d, a)
+                ntile, nkb = -(-s // 16), -(-s // keys)
+                want_bh = expected_sum_bh(bh, s, causal, keys) if d <= 64 else 0
                 assert a["bad"] == 0 and a["twice"] == 0, (s, bh, d, a)
                 assert a["covered"] == want_bh * ntile, (s, bh, d, a, want_bh)
                 if causal:
@@ -307,3 +318,6 @@ def test_step2_dq_sum_schedule(causal):
     if not causal:
         a = sum_audit(1, 17, 50, 64, False)
         assert a["covered"] == 16 * 4 and a["bad"] == 0
+        # The benchmark's shapes: config 2 (s 240) keeps 64-key blocks, config 5 (s 1024) 128.
+        assert sum_audit(64, 6, 240, 64, False)["keys"] == 64
+        assert sum_audit(16, 16, 1024, 64, False)["keys"] == 128

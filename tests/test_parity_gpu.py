@@ -657,6 +657,68 @@ def test_dq_sums_in_step2_match_step3(orc, cuda, d, h, s):
     assert np.array_equal(summed, want)
 
 
+def test_long_noncausal_128_key_blocks(orc, cuda):
+    """Non-causal d 64 from s 512 on, with at least 512 workgroups of 128 keys, step 2 runs
+    128-key blocks (each wave two groups of 16 keys; half the dQ partials). At b 4 h 32 s 512:
+    every (b, h) slice against the fp64 oracle, two runs bit-identical, and step 2's own dQ sums
+    switched off by the test hook (step 3 sums every tile) giving the same bits."""
+    from test_boundary import sum_audit
+    b, h, s = 4, 32, 512
+    assert sum_audit(b, h, s, 64, False)["keys"] == 128
+    x, dout, qkv, g = seeded_qkv(orc, b, h, s, 21, cuda)
+    say(f"128-key blocks: b{b} h{h} s{s}")
+    out, grad = run("fused_qkv", qkv, g, h, 64, False, 0.125)
+    ref_out, _, ref_grad = oracle_qkv(orc, x, dout, h, 64, False, np.float64, 0.125)
+    check_errors(orc, out, grad, ref_out, ref_grad, "b4 h32 s512")
+    out2, grad2 = run("fused_qkv", qkv, g, h, 64, False, 0.125)
+    assert torch.equal(bits(out2), bits(out)) and torch.equal(bits(grad2), bits(grad))
+    f = _lib.lib().fattn_internal_step2_sums
+    f.argtypes = [ctypes.c_int]
+    f.restype = ctypes.c_int
+    prev = f(0)
+    try:
+        _, grad3 = run("fused_qkv", qkv, g, h, 64, False, 0.125)
+    finally:
+        f(prev)
+    assert torch.equal(bits(grad3), bits(grad)), "step 2 sums off: different bits"
+    # The general entry on the head views takes the same path: the same gradient.
+    _, grad4 = run("fused", qkv, g, h, 64, False, 0.125)
+    assert torch.equal(bits(grad4), bits(grad))
+
+
+def test_long_noncausal_128_key_blocks_sum_schedule(orc, cuda):
+    """The 128-key path's dQ sums in step 2: b 1 h 128 s 512 with every head given the same q, k,
+    v and output gradient, so that every head's O and gradient must be bit-identical whichever
+    kernel summed it; after step 2 alone the done flags mark exactly the heads the schedule gives
+    the summing workgroups (all 128 here); head 0 against the fp64 oracle."""
+    from test_boundary import expected_sum_bh, sum_audit
+    h, s, d = 128, 512, 64
+    assert sum_audit(1, h, s, d, False)["keys"] == 128
+    rng = np.random.default_rng(5)
+    one = rng.standard_normal((1, s, 3, 1, d)).astype(np.float32)
+    x = np.ascontiguousarray(np.broadcast_to(one, (1, s, 3, h, d))).reshape(1, s, 3 * h * d)
+    w1 = rng.standard_normal((1, s, 1, d)).astype(np.float32)
+    w = np.ascontiguousarray(np.broadcast_to(w1, (1, s, h, d))).reshape(1, s, h * d)
+    out, grad = run("fused_qkv", torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), h, d,
+                    False, 0.125)
+    o = out.reshape(1, s, h, d)
+    gr = grad.reshape(1, s, 3, h, d)
+    for i in range(1, h):
+        assert torch.equal(bits(o[:, :, i]), bits(o[:, :, 0])), f"O of head {i}"
+        assert torch.equal(bits(gr[:, :, :, i]), bits(gr[:, :, :, 0])), f"gradient of head {i}"
+    ref_out, _, ref_grad = oracle_qkv(orc, one.reshape(1, s, 3 * d), w1.reshape(1, s, d), 1, d,
+                                      False, np.float64, 0.125)
+    check_errors(orc, o[:, :, 0].contiguous(), gr[:, :, :, 0].reshape(1, s, 3 * d), ref_out,
+                 ref_grad, "head 0")
+    summed = step2_summed_tiles(torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda), h, d,
+                                False, grad)
+    n_bh = expected_sum_bh(h, s, False, 128)
+    want = np.zeros((h, -(-s // 16)), dtype=bool)
+    want[:n_bh] = True
+    say(f"  step 2 summed {int(summed.sum())} of {summed.size} tiles (schedule: {n_bh} heads)")
+    assert n_bh == h and np.array_equal(summed, want)
+
+
 def ws_layout(b, h, s, d):
     """Byte offsets of the backward workspace's parts (restated from fattn_api.cpp's
     workspace_layout; the library's reported sizes pin it)."""
