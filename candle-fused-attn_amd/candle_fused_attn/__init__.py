@@ -13,6 +13,7 @@ from .ops import (
     float4_aligned,
     fused_attention,
     fused_attention_qkv,
+    qkv_projection_of,
     reads_in_place,
     set_dq_sum,
 )
@@ -26,6 +27,7 @@ __all__ = [
     "float4_aligned",
     "fused_attention",
     "fused_attention_qkv",
+    "qkv_projection_of",
     "reads_in_place",
     "set_dq_sum",
     "version",

@@ -8,7 +8,10 @@ from a profiler. Here every contender is Python on one device, so the design is 
 * Contenders. Each one maps the fused projection qkv [b, s, 3 h d] (a leaf tensor) to the merged
   output [b, s, h d], so head split and merge are part of every timed call:
     fattn.qkv        fused_attention_qkv (libfattn.so, hand-written gfx950 kernels)
-    fattn.views      fused_attention on the q / k / v views of qkv, output merged back
+    fattn.views      fused_attention on the q / k / v views of qkv, output merged back (the
+                     views of one projection go to fused_attention_qkv's node)
+    fattn.general    the same call with that routing switched off: fused_attention's own node,
+                     whose three gradients autograd assembles into qkv's
     torch.eager      explicit softmax((q k^T) scale) v in torch ops (hipBLASLt matmuls)
     sdpa.math        scaled_dot_product_attention with the MATH backend forced
     sdpa.efficient   ... EFFICIENT_ATTENTION backend forced (AOTriton on ROCm)
@@ -55,7 +58,7 @@ from typing import Callable
 
 PARTS = ("o", "dq", "dk", "dv")
 PHASES = ("fwd", "step")
-MINE = ("fattn.qkv", "fattn.views")
+MINE = ("fattn.qkv", "fattn.views", "fattn.general")
 SDPA_BACKENDS = {"sdpa.math": "MATH", "sdpa.efficient": "EFFICIENT_ATTENTION",
                  "sdpa.flash": "FLASH_ATTENTION"}
 
@@ -244,6 +247,13 @@ def make_contenders(heads: int, scale: float, causal: bool) -> list[Contender]:
         q, k, v = views(qkv)
         return merge(cfa.fused_attention(q, k, v, scale, causal))
 
+    def fattn_general(qkv):
+        prev = cfa.ops.set_projection_route(False)
+        try:
+            return fattn_views(qkv)
+        finally:
+            cfa.ops.set_projection_route(prev)
+
     def eager(qkv):
         q, k, v = views(qkv)
         w = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
@@ -266,6 +276,8 @@ def make_contenders(heads: int, scale: float, causal: bool) -> list[Contender]:
     out = [Contender("fattn.qkv", lambda x: cfa.fused_attention_qkv(x, heads, scale, causal),
                      "fused_attention_qkv (libfattn.so)"),
            Contender("fattn.views", fattn_views, "fused_attention on the q/k/v views"),
+           Contender("fattn.general", fattn_general,
+                     "fused_attention on the q/k/v views, its own node (no routing)"),
            Contender("torch.eager", eager, "softmax((q k^T) scale) v in torch ops")]
     for name, backend in SDPA_BACKENDS.items():
         out.append(Contender(name, sdpa_with(backend), f"scaled_dot_product_attention, {backend}"))

@@ -233,6 +233,46 @@ def fused_attention_qkv(qkv: torch.Tensor, heads: int, scale: float,
     return _FusedAttentionQkv.apply(qkv, heads, scale, causal)
 
 
+_route_projection = True
+
+
+def set_projection_route(on: bool) -> bool:
+    """Whether fused_attention hands the head-split views of one projection to the projection's
+    node (the default) or to its own general node (for tests comparing the two); returns the
+    previous setting."""
+    global _route_projection
+    prev, _route_projection = _route_projection, bool(on)
+    return prev
+
+
+def qkv_projection_of(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    """The contiguous [b, s, 3 h d] projection whose head-split views q, k, v are (q, k, v its
+    parts at element offsets 0, h d, 2 h d, strides (s 3hd, d, 3hd, 1): the layout candle-mi
+    feeds fused_attention, tests/parity.rs:38-50), or None. Only where the op on the projection
+    is the same computation with the same gradients: a head_dim the kernels take, rows
+    float4-aligned, and q, k, v differentiable views of it (not detached leaves, none retaining
+    its own gradient), so every gradient reaches the projection either way."""
+    base = q._base
+    if base is None or k._base is not base or v._base is not base or base.dim() != 3:
+        return None
+    if q.dim() != 4 or not base.is_contiguous() or base.dtype != torch.float32:
+        return None
+    b, h, s, d = q.shape
+    if d not in HIP_HEAD_DIMS or tuple(base.shape) != (b, s, 3 * h * d) or not _qkv_aligned(base):
+        return None
+    for i, t in enumerate((q, k, v)):
+        if (tuple(t.shape) != (b, h, s, d) or t.stride() != (s * 3 * h * d, d, 3 * h * d, 1)
+                or t.storage_offset() - base.storage_offset() != i * h * d):
+            return None
+        if not torch.is_grad_enabled():
+            continue  # no graph is recorded: nothing to route
+        if t.requires_grad != base.requires_grad or t.retains_grad:
+            return None
+        if t.requires_grad and t.grad_fn is None:
+            return None
+    return base
+
+
 def fused_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
                     causal: bool) -> torch.Tensor:
     """Fused scaled-dot-product attention: softmax(q k^T scale) v, keys after the query masked
@@ -241,9 +281,20 @@ def fused_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
     q, k, v: [batch, heads, seq, head_dim] f32 on one HIP device, any strides (copied first when
     the kernels cannot read them in place). Returns [batch, heads, seq, head_dim], a transposed
     view of a contiguous [batch, seq, heads, head_dim] buffer.
+
+    When q, k, v are the head-split views of one contiguous [b, s, 3 h d] projection, the op is
+    applied to the projection itself (fused_attention_qkv's node, the same kernels and bits):
+    its gradient is the backward's one [b, s, 3, h, d] buffer, where three view gradients would
+    make autograd copy them back into a projection-shaped tensor (at b 64, s 240, h 6, d 64: a
+    70.8 MB copy and an add, 72 us of a 200 us step).
     """
     _require("fused_attention", "q", q)
     _require("fused_attention", "k", k, q.device)
     _require("fused_attention", "v", v, q.device)
+    base = qkv_projection_of(q, k, v) if _route_projection else None
+    if base is not None:
+        b, h, s, d = q.shape
+        out = _FusedAttentionQkv.apply(base, h, scale, causal)
+        return out.view(b, s, h, d).transpose(1, 2)
     q, k, v = float4_rows(q), float4_rows(k), float4_rows(v)
     return _FusedAttention.apply(q, k, v, scale, causal).transpose(1, 2)

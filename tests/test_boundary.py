@@ -224,6 +224,38 @@ def test_alignment_predicates():
     assert cfa.CUDA_HEAD_DIM == 64 and cfa.HIP_HEAD_DIMS == (32, 64, 128)
 
 
+def test_projection_views_predicate():
+    """fused_attention routes q, k, v to the projection's op only when they are exactly its
+    head-split views and every gradient would reach the projection either way."""
+    b, s, h, d = 2, 5, 3, 64
+
+    def views(qkv):
+        x = qkv.view(b, s, 3, h, d)
+        return [x[:, :, i].transpose(1, 2) for i in range(3)]
+
+    qkv = torch.zeros(b, s, 3 * h * d, requires_grad=True)
+    q, k, v = views(qkv)
+    assert cfa.qkv_projection_of(q, k, v) is qkv
+    with torch.no_grad():                                 # inference: no gradients to route
+        assert cfa.qkv_projection_of(*views(qkv)) is qkv
+    assert cfa.qkv_projection_of(q, v, k) is None         # parts out of order
+    assert cfa.qkv_projection_of(q, k, k) is None
+    other = torch.zeros(b, s, 3 * h * d)
+    assert cfa.qkv_projection_of(q, k, views(other)[2]) is None       # another projection
+    q2 = q.detach().requires_grad_(True)                  # a leaf of its own: keeps its gradient
+    assert cfa.qkv_projection_of(q2, k, v) is None
+    q3, k3, v3 = views(qkv)
+    q3.retain_grad()                                      # a view that keeps its own gradient
+    assert cfa.qkv_projection_of(q3, k3, v3) is None
+    wide = torch.zeros(b, s, 3 * h * d + 4)[..., : 3 * h * d]       # not a contiguous projection
+    parts = [wide[..., i * h * d:(i + 1) * h * d].unflatten(-1, (h, d)).transpose(1, 2)
+             for i in range(3)]
+    assert cfa.qkv_projection_of(*parts) is None
+    odd = torch.zeros(b, s, 3 * 3 * 48)                   # head_dim 48: not a kernel's
+    x48 = odd.view(b, s, 3, 3, 48)
+    assert cfa.qkv_projection_of(*[x48[:, :, i].transpose(1, 2) for i in range(3)]) is None
+
+
 def test_slice_offsets_must_fit_32_bits():
     """The kernels address one (batch, head) slice with 32-bit offsets: a slice spanning more
     than 4 GiB is refused up front (no launch)."""

@@ -55,11 +55,18 @@ def qkv_views(qkv, h, d):
 
 
 def attend(path, qkv, h, d, causal, scale=None):
+    """path "fused": fused_attention's general node on the head views; "fused_views": the same
+    call as a user makes it (the views go to the projection's node); "fused_qkv":
+    fused_attention_qkv."""
     b, s, _ = qkv.shape
     scale = 1.0 / d ** 0.5 if scale is None else scale
-    if path == "fused":
+    if path in ("fused", "fused_views"):
         q, k, v = qkv_views(qkv, h, d)
-        o = cfa.fused_attention(q, k, v, scale, causal)
+        prev = cfa.ops.set_projection_route(path == "fused_views")
+        try:
+            o = cfa.fused_attention(q, k, v, scale, causal)
+        finally:
+            cfa.ops.set_projection_route(prev)
         return o.transpose(1, 2).reshape(b, s, h * d)
     return cfa.fused_attention_qkv(qkv, h, scale, causal)
 
@@ -717,6 +724,30 @@ def test_long_noncausal_128_key_blocks_sum_schedule(orc, cuda):
     want[:n_bh] = True
     say(f"  step 2 summed {int(summed.sum())} of {summed.size} tiles (schedule: {n_bh} heads)")
     assert n_bh == h and np.array_equal(summed, want)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_projection_views_take_the_qkv_node(orc, cuda, causal):
+    """fused_attention on the head-split views of one projection runs fused_attention_qkv's node:
+    its output and the projection's gradient equal both the qkv entry's and the general node's bit
+    for bit, the graph holds the projection's node, and no view gradient is assembled."""
+    b, h, s, d = 4, 6, 240, 64
+    x, dout, qkv, g = seeded_qkv(orc, b, h, s, 7, cuda)
+    res = {p: run(p, qkv, g, h, d, causal, 0.125) for p in ("fused_views", "fused_qkv", "fused")}
+    for p in ("fused_qkv", "fused"):
+        assert torch.equal(bits(res["fused_views"][0]), bits(res[p][0])), f"O vs {p}"
+        assert torch.equal(bits(res["fused_views"][1]), bits(res[p][1])), f"gradient vs {p}"
+    xx = qkv.detach().clone().requires_grad_(True)
+    q, k, v = qkv_views(xx, h, d)
+    out = cfa.fused_attention(q, k, v, 0.125, causal)
+    names = []
+    fn = out.grad_fn
+    while fn is not None and len(names) < 8:
+        names.append(type(fn).__name__)
+        fn = fn.next_functions[0][0] if fn.next_functions else None
+    say(f"  graph from the output: {names}")
+    assert any("FusedAttentionQkv" in n for n in names), names
+    assert not any(n == "_FusedAttentionBackward" for n in names), names
 
 
 def ws_layout(b, h, s, d):
