@@ -993,3 +993,74 @@ def test_scale_signs(orc, cuda, causal):
             want = np.broadcast_to(np.log(n.astype(np.float64)), (b, h, s))
             got = lse.cpu().numpy().astype(np.float64)
             assert np.max(np.abs(got - want)) <= 4e-7 * np.log(s), "L = ln n at scale 0"
+
+
+# --- operand layouts at random: fused_attention on views the kernels read in place or copy -----
+
+LAYOUTS = ("contig", "bshd", "sbhd", "padded", "misaligned", "oddrow")
+
+
+def layout_of(kind, vals, rng, cuda):
+    """A [b, h, s, d] leaf on the device holding `vals` (float32, C order) in one of the layouts a
+    candle caller hands fused_attention: contiguous; a transposed view of [b, s, h, d] (the
+    merge-heads layout); a permuted view of [s, b, h, d]; rows padded to d + 4 or d + 8 floats;
+    storage offset 1 (not float4-aligned: copied); rows of d + 1 floats (not float4-aligned:
+    copied). The bases are made on the device, so the views keep their strides."""
+    b, h, s, d = vals.shape
+    t = torch.from_numpy(vals).to(cuda)
+    if kind == "contig":
+        v = t.clone()
+    elif kind == "bshd":
+        v = t.transpose(1, 2).contiguous().transpose(1, 2)
+    elif kind == "sbhd":
+        v = t.permute(2, 0, 1, 3).contiguous().permute(1, 2, 0, 3)
+    elif kind in ("padded", "oddrow"):
+        pad = int(rng.choice([4, 8])) if kind == "padded" else 1
+        base = torch.zeros(b, h, s, d + pad, device=cuda)
+        base[..., :d] = t
+        v = base[..., :d]
+    else:
+        base = torch.zeros(t.numel() + 1, device=cuda)
+        base[1:] = t.reshape(-1)
+        v = base[1:].view(b, h, s, d)
+    assert torch.equal(v, t), kind
+    assert cfa.reads_in_place(v) == (kind not in ("misaligned", "oddrow")), kind
+    return v.detach().requires_grad_(True)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_random_layouts(orc, cuda, seed):
+    """fused_attention on q, k, v and an output gradient in layouts drawn at random (each operand
+    its own), at random b, h, s (1-160), head_dim (32, 64, 128), mask and scale (either sign):
+    output and the three gradients against the fp64 oracle (src/lib.rs:241-299) at the bar of the
+    other parity tests -- within 2e-6 normwise or 1.5x the fp32 composed path's own error."""
+    rng = np.random.default_rng(1000 + seed)
+    b, h = int(rng.integers(1, 4)), int(rng.integers(1, 6))
+    s, d = int(rng.integers(1, 161)), int(rng.choice([32, 64, 128]))
+    causal = bool(rng.integers(0, 2))
+    scale = float(rng.choice([-1.0, 1.0]) * rng.uniform(0.05, 0.3))
+    kinds = [str(rng.choice(LAYOUTS)) for _ in range(4)]
+    say(f"seed {seed}: b {b} h {h} s {s} d {d} causal={causal} scale {scale:.4f} layouts {kinds}")
+    vals = [rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(4)]
+    q, k, v, w = (layout_of(kd, x, rng, cuda) for kd, x in zip(kinds, vals))
+    out = cfa.fused_attention(q, k, v, scale, causal)
+    (out * w.detach()).sum().backward()
+    torch.cuda.synchronize()
+    got = {"o": out.detach().cpu().numpy(), "dq": q.grad.cpu().numpy(),
+           "dk": k.grad.cpu().numpy(), "dv": v.grad.cpu().numpy()}
+    qn, kn, vn, wn = vals
+    ref, floor = {}, {}
+    for dtype, dst in ((np.float64, ref), (np.float32, floor)):
+        o, l_ = orc.forward(qn, kn, vn, scale, causal, dtype)
+        dq, dk, dv = orc.backward(qn, kn, vn, o, l_, wn, scale, causal, dtype)
+        dst.update(o=o, dq=dq, dk=dk, dv=dv)
+    for name in ("o", "dq", "dk", "dv"):
+        r = np.asarray(ref[name], dtype=np.float64)
+        if not np.any(r):
+            dev = float(np.abs(got[name]).max())
+            assert dev <= BAND, f"{name} (exactly zero in fp64) max deviation {dev:.3e}"
+            continue
+        err = orc.rel_fro(got[name], r)
+        tol = max(REL_TOL, 1.5 * orc.rel_fro(floor[name], r))
+        say(f"  {name}: {err:.2e} (bar {tol:.2e})")
+        assert err <= tol, f"{name}: normwise error {err:.3e} > {tol:.3e}"
