@@ -8,11 +8,12 @@ config 2's synthetic inputs (qkv [64, 240, 1152] ~ N(0, 1) and dout [64, 240, 38
 by a CPU torch generator seeded 0, the reference's published inputs), resident in HBM before the
 timed region. The op-level C ABI is called with preallocated outputs on torch's current stream.
 
-Configs 3-5 (causal, long causal, strided views) are timed too, as extra keys of the same line
-(`configs`): op-level forward and forward+backward, and each kernel on its own.
+Configs 3-5 (causal, long causal, strided views) and config 2's shape at head_dim 32 and 128
+are timed too, as extra keys of the same line (`configs`): op-level forward and
+forward+backward, and each kernel on its own.
 
 Order of the GPU work: W warm-up + K timed steps from an idle GPU (`fwd_bwd_from_idle_ms`),
-configs 3-5, then W warm-up + K timed steps (`value`), K forwards (`fwd_ms`) and K kernel-level
+configs 3-5 and the two head_dims, then W warm-up + K timed steps (`value`), K forwards (`fwd_ms`) and K kernel-level
 steps (`kernels_us`, `roofline`). MI355X runs at lower clocks for some tens of milliseconds after
 an idle second, so the headline steps come right after sustained work, as in a training loop; the
 from-idle figure shows what a short run on an idle GPU sees.
@@ -161,21 +162,22 @@ class Workload:
                 _lib.check(L.fattn_backward(*args, SCALE, ci, P(out), P(lse), dout_p, 0, gshape,
                                             gstrides, P(dqkv), P(ws), ws_bytes, sp))
 
+        # The kernel-level entries: the reference's names at d 64, the general ones elsewhere.
+        kl = {n: getattr(L, f"fattn_{n}_f32_d64" if d == 64 else f"fattn_{n}_f32")
+              for n in ("fwd", "bwd_prep", "bwd_main", "bwd_dq")}
+
         def fwd_k():
-            _lib.check(L.fattn_fwd_f32_d64(*views, P(out), P(lse), b, h, s, d, SCALE, ci, *vst,
-                                           sp))
+            _lib.check(kl["fwd"](*views, P(out), P(lse), b, h, s, d, SCALE, ci, *vst, sp))
 
         def prep_k():
-            _lib.check(L.fattn_bwd_prep_f32_d64(P(out), dout_p, gst, P(ws), ws_bytes, b, h, s, d,
-                                                sp))
+            _lib.check(kl["bwd_prep"](P(out), dout_p, gst, P(ws), ws_bytes, b, h, s, d, sp))
 
         def main_k():
-            _lib.check(L.fattn_bwd_main_f32_d64(*views, P(out), dout_p, P(lse), P(dqkv), P(ws),
-                                                ws_bytes, b, h, s, d, SCALE, ci, *vst, gst, sp))
+            _lib.check(kl["bwd_main"](*views, P(out), dout_p, P(lse), P(dqkv), P(ws), ws_bytes,
+                                      b, h, s, d, SCALE, ci, *vst, gst, sp))
 
         def dq_k():
-            _lib.check(L.fattn_bwd_dq_f32_d64(P(dqkv), P(ws), ws_bytes, b, h, s, d, SCALE, ci,
-                                              sp))
+            _lib.check(kl["bwd_dq"](P(dqkv), P(ws), ws_bytes, b, h, s, d, SCALE, ci, sp))
 
         self.fwd, self.bwd = fwd, bwd
         # With a split workspace at d 64 step 1 launches nothing (step 2 computes D itself, and
@@ -380,7 +382,8 @@ def main() -> int:
     ap.add_argument("--causal", action="store_true", help="config 3 as the main workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-accuracy", action="store_true", help="skip the fp64 scoring")
-    ap.add_argument("--no-extra", action="store_true", help="skip timing configs 3-5")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip timing configs 3-5 and config 2 at head_dim 32 / 128")
     ap.add_argument("--extra-steps", type=int, default=20)
     ap.add_argument("--cpu-threads", type=int, default=None)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -454,6 +457,12 @@ def main() -> int:
             extra[f"config{cfg}"] = time_extra(torch, xw, max(args.extra_steps, 1), 100)
             log(f"bench: {CONFIGS[cfg][0]}: {json.dumps(extra[f'config{cfg}'])}")
             del xw
+        # The other head dims the kernels are built for, at the headline's shape.
+        for d in (32, 128):
+            xw = Workload(torch, L, _lib, dev, 2, d=d)
+            extra[f"config2_d{d}"] = time_extra(torch, xw, max(args.extra_steps, 1), 100)
+            log(f"bench: config 2 at d {d}: {json.dumps(extra[f'config2_d{d}'])}")
+            del xw
         torch.cuda.synchronize()
 
     for _ in range(max(args.warmup, 1)):
@@ -521,7 +530,8 @@ def main() -> int:
         "fwd_bwd_from_idle_first5_ms": round(statistics.mean(cold_steps[:n5]), 5),
         "fwd_bwd_from_idle_last5_ms": round(statistics.mean(cold_steps[-n5:]), 5),
         "sequence": ("W warm-up + K timed steps from idle (fwd_bwd_from_idle_ms), "
-                     + ("configs 3-5 timed (configs), " if extra else "")
+                     + ("configs 3-5 and config 2 at d 32 / 128 timed (configs), "
+                        if extra else "")
                      + "W warm-up + K timed steps (value), K forwards, K kernel-level steps"),
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_bwd_tflops": round(total_tflops, 3),
