@@ -1428,7 +1428,14 @@ bwd_split_kernel(BwdArgs a) {
     if (id >= a.n_main) bwd_sum_tiles<D>(a, id & 7, (id - a.n_main) >> 3, &sm.flag);
     return;
   }
-  const bool wave_dq = w < kDT;  // the wave computes dQ tiles (all waves but 2, 3 at D 32)
+  // The dQ product's 16-dim tiles: D / 16 of them for four waves. At D 64 wave w takes tile w on
+  // every query tile; at D 32 waves 0, 1 take the two tiles on one query tile and waves 2, 3 on
+  // the next (the turn alternating with the workgroup's parity as well), so that each SIMD gets
+  // the same share of the products (with waves 0, 1 always, SIMDs 2, 3 idled a third of the
+  // time at D 32). Who computes a fragment changes nothing in it.
+  constexpr int kDqGroups = 4 / kDT;
+  const int dt = w % kDT;
+  auto dq_on = [&](int jt) { return kDqGroups == 1 || w / kDT == (jt + id) % kDqGroups; };
   // No turn waits here: the guard word reads 0.
   if (id == 0 && tid == 0) a.ctrl[kCtrlGuard] = 0;
 
@@ -1473,7 +1480,7 @@ bwd_split_kernel(BwdArgs a) {
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
         const int kk = k0 + 64 * hh + 16 * g + t;
-        kQ[hh][t] = kk < S && wave_dq ? kp[min(kk, S - 1) * a.k.ss + 16 * w + lo] : 0.0f;
+        kQ[hh][t] = kk < S ? kp[min(kk, S - 1) * a.k.ss + 16 * dt + lo] : 0.0f;
       }
     }
   }
@@ -1518,11 +1525,11 @@ bwd_split_kernel(BwdArgs a) {
     }
   };
 
-  // The dQ partial of query tile j: the wave's 16 x 16 fragment (dim tile w) in the key block's
+  // The dQ partial of query tile j: the wave's 16 x 16 fragment (dim tile dt) in the key block's
   // slot, fragment order (register r of lane (lo, g) at 4 lane + r: query 16 j + 4 g + r, dim
-  // 16 w + lo); step 3 (dq_kernel) sums the slots.
+  // 16 dt + lo); step 3 (dq_kernel) sums the slots.
   float* const slot = a.part + (static_cast<int64_t>(kb) * BH + bh) * a.ntile * (kQT * D) +
-                      256 * w + 4 * lane;
+                      256 * dt + 4 * lane;
 
   f4 dva[KG][kDT], dka[KG][kDT];
 #pragma unroll
@@ -1562,7 +1569,7 @@ bwd_split_kernel(BwdArgs a) {
     const int q0 = jt * kQT;
     // Tile t + 2 into the buffer of tile t - 1, whose last readers passed the last barrier.
     if (t + 2 < nsteps) gload(t + 2, Const<(buf + 2) % kNB>{});
-    const bool frag_pending = t > 0 && wave_dq;  // the last tile's fragment is unstored
+    const bool frag_pending = t > 0 && dq_on(jt - 1);  // the last tile's fragment is unstored
     if (frag_pending) store_frag(jt - 1);
     compiler_fence();
     const float* Qt = sQ[buf];
@@ -1652,9 +1659,9 @@ bwd_split_kernel(BwdArgs a) {
     }
     __syncthreads();  // dS complete; tile t + 2's rows landed
 
-    // The dQ partial dS K over the block's keys (the wave's dim tile w).
+    // The dQ partial dS K over the block's keys (the wave's dim tile dt, if its turn).
     p1 = zero4();
-    if (q0 < S && wave_dq) {
+    if (q0 < S && dq_on(jt)) {
 #pragma unroll
       for (int hh = 0; hh < KG; ++hh) {
 #pragma unroll
@@ -1676,7 +1683,7 @@ bwd_split_kernel(BwdArgs a) {
     if (t + 1 < nsteps) tile_step(Const<1>{}, t + 1);
     if (t + 2 < nsteps) tile_step(Const<2>{}, t + 2);
   }
-  if (wave_dq) store_frag(t0 + nsteps - 1);  // the last tile's fragment
+  if (dq_on(t0 + nsteps - 1)) store_frag(t0 + nsteps - 1);  // the last tile's fragment
   if (a.arrive != nullptr) {
     // Every partial of this key block is stored once the stores of every wave have completed:
     // record its arrival, with the XCD it runs on (dK and dV, stored below, are not read by the
