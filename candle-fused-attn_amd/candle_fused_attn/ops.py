@@ -117,7 +117,10 @@ def set_dq_sum(mode: str) -> str:
       "split": each key block writes its partials to the workspace (about 4 s^2 b h bytes) and a
                third kernel sums them -- no workgroup waits on another;
       "turns": key blocks add into dQ in place under turn counters (minimum workspace);
-      "auto" (default): "split" unless its workspace exceeds the library's FATTN_SPLIT_MAX_BYTES.
+      "auto" (default): "split" unless its workspace exceeds the library's FATTN_SPLIT_MAX_BYTES;
+               then, at head_dim <= 64, "split" by chunks of (b, h) pairs (each chunk's state in
+               a workspace within that size; the same results) where the chunks fill the chip,
+               else "turns".
     """
     global _dq_sum
     if mode not in _DQ_SUM_MODES:

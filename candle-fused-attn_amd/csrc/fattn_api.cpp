@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <numeric>
 #include <atomic>
 #include <chrono>
 #include <cstdint>
@@ -25,10 +26,12 @@ Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d) {
   const size_t rows = static_cast<size_t>(b * h * s);
   const size_t tiles = static_cast<size_t>(b * h * ((s + kBwdQueryTile - 1) / kBwdQueryTile));
   const size_t nkb = static_cast<size_t>((s + kBwdKeys - 1) / kBwdKeys);
-  w.d_off = 0;
-  w.turn_off = up(rows * sizeof(float));
-  w.ctrl_off = w.turn_off + up(tiles * sizeof(int));
-  w.part_off = w.ctrl_off + up(64 * sizeof(int));
+  // The control words (ticket, guard word) first: their place is the same for every shape, so
+  // fattn_bwd_status finds the guard word whichever way the workspace was used.
+  w.ctrl_off = 0;
+  w.d_off = up(64 * sizeof(int));
+  w.turn_off = w.d_off + up(rows * sizeof(float));
+  w.part_off = w.turn_off + up(tiles * sizeof(int));
   w.bytes_min = w.part_off;
   w.arrive_off = w.part_off + up(nkb * tiles * kBwdQueryTile * static_cast<size_t>(d) *
                                  sizeof(float));
@@ -36,6 +39,74 @@ Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d) {
   w.epoch_off = w.done_off + up(tiles * sizeof(unsigned long long));
   w.bytes_split = w.epoch_off + 256;
   return w;
+}
+
+// The (b, h) pairs per chunk of the split dQ sum that a workspace of ws_bytes holds: b h when it
+// holds the whole split; else, at d <= 64, from the most pairs whose split partials, arrival
+// slots and done flags fit:
+//   causal: equal chunks, a multiple of 8 from 8 on (then a chunk's key blocks of one (b, h) share
+//     an XCD, as its own sums need);
+//   non-causal: the most pairs whose key blocks fill whole rounds of the chip's workgroup slots
+//     (every key block walks all query tiles, so a partial round idles slots; the last chunk
+//     takes the rest);
+// 0 when that is fewer than min_pairs. Steps 2 and 3 then run per chunk, each chunk's state at
+// the start of the workspace (workspace_layout(1, chunk, s, d)).
+int64_t split_chunk(int64_t b, int64_t h, int64_t s, int64_t d, size_t ws_bytes,
+                    int64_t min_pairs, bool causal) {
+  const int64_t total = b * h;
+  if (workspace_layout(b, h, s, d).bytes_split <= ws_bytes) return total;
+  if (d > 64) return 0;
+  int64_t lo = 0, hi = total - 1;  // the split size grows with the pair count
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (workspace_layout(1, mid, s, d).bytes_split <= ws_bytes) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  if (!causal) {
+    // Key blocks per pair, and the slots they fill: 128-key blocks run 2 workgroups per CU,
+    // 64-key blocks 3 (256 CUs on gfx950).
+    const int keys = bwd_split_keys(b, h, s, static_cast<int>(d), 0);
+    const int64_t nkb = (s + keys - 1) / keys, slots = (keys > kBwdKeys ? 2 : 3) * int64_t{256};
+    const int64_t quantum = slots / std::gcd(slots, nkb);
+    if (lo >= quantum) lo -= lo % quantum;
+    return lo == 0 || lo < min_pairs ? 0 : lo;
+  }
+  const bool round8 = lo >= 8;
+  if (round8) lo &= ~int64_t{7};
+  if (lo == 0 || lo < min_pairs) return 0;
+  // Equal chunks: ceil(total / chunks) <= lo, and a multiple of 8 up to lo stays <= lo.
+  const int64_t chunks = (total + lo - 1) / lo;
+  int64_t c = (total + chunks - 1) / chunks;
+  if (round8) c = (c + 7) & ~int64_t{7};
+  return c;
+}
+
+// The fewest (b, h) pairs a chunk should hold. A chunk is one launch of step 2: with too few key
+// blocks it runs at a fraction of the chip, so chunks of fewer pairs than this lose to the turn
+// hand-over over all pairs (measured: b 4 h 16 s 8192 causal, chunks of 8 pairs 15.1 ms against
+// 13.8 with turns). Non-causal: the chunk's key blocks fill the chip's workgroup slots (3 per CU,
+// 256 CUs on gfx950) at least once. Causal: the key blocks' walks shrink with the block index, so
+// the slots' average work must be at least twice the longest walk (block 0's, all query tiles):
+// four times the slots in key blocks.
+int64_t min_chunk_pairs(int64_t s, bool causal) {
+  constexpr int64_t kSlots = 3 * 256;
+  const int64_t nkb = (s + kBwdKeys - 1) / kBwdKeys;
+  const int64_t blocks = causal ? 4 * kSlots : kSlots;
+  return (blocks + nkb - 1) / nkb;
+}
+
+// The workspace the library asks for within `limit` bytes: the whole split, else the split of the
+// largest chunk that is worth it (non-causal measure: the size takes no mask), else the turn
+// hand-over's minimum (possibly over the limit: the caller decides).
+size_t workspace_within(int64_t b, int64_t h, int64_t s, int64_t d, size_t limit) {
+  const Workspace l = workspace_layout(b, h, s, d);
+  if (l.bytes_split <= limit) return l.bytes_split;
+  // (sized with the causal rule, whose chunk sizes the non-causal rule's fit too)
+  const int64_t c = split_chunk(b, h, s, d, limit, min_chunk_pairs(s, false), true);
+  return c > 0 ? workspace_layout(1, c, s, d).bytes_split : l.bytes_min;
 }
 
 }  // namespace fattn
@@ -212,9 +283,9 @@ int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_
   return ok();
 }
 
-int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d_o,
-                 const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
-                 int64_t s, int64_t d, float scale, int causal, void* stream) {
+// Step 2's operand checks (nothing launched).
+int check_bwd_main(const char* who, View q, View k, View v, const float* o, View d_o,
+                   const float* lse, float* dqkv, int64_t b, int64_t h, int64_t s, int64_t d) {
   if (int rc = check_range(who, b, h, s, d)) return rc;
   if (!slice_fits(q, s, d) || !slice_fits(k, s, d) || !slice_fits(v, s, d) ||
       !slice_fits(d_o, s, d) || s * 3 * h * d > int64_t{UINT32_MAX}) {
@@ -227,13 +298,20 @@ int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d
       !aligned16(o) || !aligned16(dqkv)) {
     return fail(FATTN_EALIGN, std::string(who) + ": rows must be 16-byte aligned");
   }
+  return 0;
+}
+
+int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d_o,
+                 const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
+                 int64_t s, int64_t d, float scale, int causal, void* stream) {
+  if (int rc = check_bwd_main(who, q, k, v, o, d_o, lse, dqkv, b, h, s, d)) return rc;
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
   const int err = fattn::launch_bwd_main(q, k, v, d_o, o, lse, p.dsum, dqkv, p.part, p.arrive,
                                          p.done, p.epoch, next_epoch(), p.turn, p.ctrl,
                                          static_cast<int>(b), static_cast<int>(h),
                                          static_cast<int>(s), static_cast<int>(d), scale,
-                                         causal ? 1 : 0, stream);
+                                         causal ? 1 : 0, 0, static_cast<int>(b * h), stream);
   if (err) return hip_fail(err, "backward step 2 launch");
   return ok();
 }
@@ -253,14 +331,56 @@ int run_bwd_dq(const char* who, float* dqkv, void* ws, size_t ws_bytes, int64_t 
   const int err = fattn::launch_bwd_dq(p.part, p.done, p.arrive, p.epoch, dqkv,
                                        static_cast<int>(b), static_cast<int>(h),
                                        static_cast<int>(s), static_cast<int>(d), scale,
-                                       causal ? 1 : 0, stream);
+                                       causal ? 1 : 0, 0, static_cast<int>(b * h), stream);
   if (err) return hip_fail(err, "backward step 3 launch");
+  return ok();
+}
+
+// Steps 2 and 3 of the split sum over the (b, h) in chunks of `chunk` pairs, each chunk's
+// partials, arrival slots and done flags at the start of the workspace (no step 1 at d <= 64).
+int run_backward_chunked(const char* who, View q, View k, View v, const float* o, View d_o,
+                         const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b,
+                         int64_t h, int64_t s, int64_t d, float scale, int causal, int64_t chunk,
+                         void* stream) {
+  if (int rc = check_bwd_main(who, q, k, v, o, d_o, lse, dqkv, b, h, s, d)) return rc;
+  WsParts p{};
+  if (int rc = workspace_parts(who, ws, ws_bytes, 1, chunk, s, d, &p)) return rc;
+  if (!p.part) return fail(FATTN_EWORKSPACE, std::string(who) + ": workspace too small");
+  for (int64_t bh0 = 0; bh0 < b * h; bh0 += chunk) {
+    const int n = static_cast<int>(std::min(chunk, b * h - bh0));
+    int err = fattn::launch_bwd_main(q, k, v, d_o, o, lse, p.dsum, dqkv, p.part, p.arrive, p.done,
+                                     p.epoch, next_epoch(), p.turn, p.ctrl, static_cast<int>(b),
+                                     static_cast<int>(h), static_cast<int>(s),
+                                     static_cast<int>(d), scale, causal ? 1 : 0,
+                                     static_cast<int>(bh0), n, stream);
+    if (err) return hip_fail(err, "backward step 2 launch");
+    err = fattn::launch_bwd_dq(p.part, p.done, p.arrive, p.epoch, dqkv, static_cast<int>(b),
+                               static_cast<int>(h), static_cast<int>(s), static_cast<int>(d),
+                               scale, causal ? 1 : 0, static_cast<int>(bh0), n, stream);
+    if (err) return hip_fail(err, "backward step 3 launch");
+  }
   return ok();
 }
 
 int run_backward(const char* who, View q, View k, View v, const float* o, View d_o,
                  const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
                  int64_t s, int64_t d, float scale, int causal, void* stream) {
+  // A workspace that holds the split sum of some (b, h) but not of all: the split sum by chunks
+  // where the chunks are large enough to beat the turn hand-over (or the workspace is too small
+  // for the turn hand-over's minimum).
+  if (int rc = check_range(who, b, h, s, d)) return rc;
+  int64_t chunk = 0;
+  if (ws) {
+    chunk = fattn::split_chunk(b, h, s, d, ws_bytes, fattn::min_chunk_pairs(s, causal != 0),
+                               causal != 0);
+    if (chunk == 0 && ws_bytes < fattn::workspace_layout(b, h, s, d).bytes_min) {
+      chunk = fattn::split_chunk(b, h, s, d, ws_bytes, 1, causal != 0);
+    }
+  }
+  if (chunk > 0 && chunk < b * h) {
+    return run_backward_chunked(who, q, k, v, o, d_o, lse, dqkv, ws, ws_bytes, b, h, s, d, scale,
+                                causal, chunk, stream);
+  }
   if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, d, stream)) return rc;
   if (int rc = run_bwd_main(who, q, k, v, o, d_o, lse, dqkv, ws, ws_bytes, b, h, s, d, scale,
                             causal, stream)) {
@@ -339,8 +459,7 @@ const char* fattn_version(void) {
 
 size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s, int64_t d) {
   if (b < 0 || h < 0 || s < 0 || !fattn::head_dim_supported(d)) return 0;
-  const fattn::Workspace l = fattn::workspace_layout(b, h, s, d);
-  return l.bytes_split <= FATTN_SPLIT_MAX_BYTES ? l.bytes_split : l.bytes_min;
+  return fattn::workspace_within(b, h, s, d, FATTN_SPLIT_MAX_BYTES);
 }
 
 size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s, int64_t d) {
@@ -435,8 +554,7 @@ int fattn_bwd_f32_noalloc(const float* q, const float* k, const float* v, const 
   }
   if (int rc = check_range(who, b, h, s, d)) return rc;
   // The split sum when its workspace fits in the scratch, else the turn hand-over.
-  const fattn::Workspace l = fattn::workspace_layout(b, h, s, d);
-  const size_t need = l.bytes_split <= FATTN_STATIC_SCRATCH_BYTES ? l.bytes_split : l.bytes_min;
+  const size_t need = fattn::workspace_within(b, h, s, d, FATTN_STATIC_SCRATCH_BYTES);
   if (need > FATTN_STATIC_SCRATCH_BYTES) {
     return fail(FATTN_EWORKSPACE,
                 std::string(who) + ": the backward of " + std::to_string(b) + " x " +
@@ -707,16 +825,18 @@ int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, i
   if (!status) return fail(FATTN_EINVAL, "fused_attention: null status");
   *status = 0;
   if (b < 0 || h < 0 || s < 0) return fail(FATTN_EINVAL, "fused_attention: negative size");
-  WsParts p{};
-  // The guard word's place does not depend on head_dim.
-  if (int rc = workspace_parts("fused_attention", const_cast<void*>(workspace), workspace_bytes,
-                               b, h, s, fattn::kHeadDim, &p)) {
-    return rc;
+  // The control words open every workspace layout (whole, chunked, minimum): the guard word's
+  // place depends on nothing else.
+  if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0 ||
+      workspace_bytes < 64 * sizeof(int)) {
+    return fail(FATTN_EWORKSPACE, "fused_attention: the backward needs a 256-byte aligned "
+                                  "workspace of at least 256 bytes");
   }
   hipError_t err = hipStreamSynchronize(static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return hip_fail(err, "status sync");
   int guard = 0;
-  err = hipMemcpy(&guard, p.ctrl + fattn::kCtrlGuard, sizeof(int), hipMemcpyDeviceToHost);
+  err = hipMemcpy(&guard, static_cast<const int*>(workspace) + fattn::kCtrlGuard, sizeof(int),
+                  hipMemcpyDeviceToHost);
   if (err != hipSuccess) return hip_fail(err, "status copy");
   *status = guard;
   return ok();

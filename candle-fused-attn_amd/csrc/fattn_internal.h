@@ -133,16 +133,19 @@ int launch_bwd_prep(const float* o, View d_o, float* dsum, int* turn, int* ctrl,
 // part == nullptr: the turn hand-over (dQ final after step 2; D from step 1); else the split
 // partials, which step 3 (launch_bwd_dq) sums into dQ (D computed from o here, no step 1).
 // arrive / done / epoch_slot (split, d <= 64): step 2's dQ sums, tagged with `epoch`.
+// bh0, nbh (split, d <= 64): the (b, h) pairs bh0 .. bh0 + nbh - 1 only, whose partials, slots
+// and flags sit in a workspace laid out for nbh pairs (workspace_layout(1, nbh, s, d)); otherwise
+// 0 and b h.
 int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const float* lse,
                     const float* dsum, float* dqkv, float* part, unsigned long long* arrive,
                     unsigned long long* done, unsigned long long* epoch_slot,
                     unsigned long long epoch, int* turn, int* ctrl, int b, int h, int s, int d,
-                    float scale, int causal, void* stream);
+                    float scale, int causal, int bh0, int nbh, void* stream);
 // Step 3: dQ of every query tile that step 2 did not sum (done: null, none did); then the done
-// flags and arrival slots are zeroed.
+// flags and arrival slots are zeroed. bh0, nbh: as step 2's.
 int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long long* arrive,
                   const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
-                  float scale, int causal, void* stream);
+                  float scale, int causal, int bh0, int nbh, void* stream);
 
 // The device address of the library's static scratch (FATTN_STATIC_SCRATCH_BYTES, the workspace
 // of fattn_bwd_f32_noalloc) on the device that runs `stream`; a hipError_t value as int.

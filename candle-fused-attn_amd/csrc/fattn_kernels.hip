@@ -743,6 +743,10 @@ struct BwdArgs {
   int causal;
   int stagger;  // non-causal only: spread the key blocks' walks over the tiles (see below)
   int kkeys;    // keys per key block (split: 64 KG)
+  // The (b, h) this launch covers: bh0 .. bh0 + nbh - 1 (the split path may run the (b, h) in
+  // chunks, each with its partials, arrival slots and done flags at the start of the workspace;
+  // the turn path always covers all, bh0 0 and nbh b h).
+  int bh0, nbh;
 };
 
 // Staggered walks make a key block wait on blocks of its own (b, h) that hold later tickets; that
@@ -1299,7 +1303,7 @@ template <int D, int NT>
 __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, int j1,
                                               unsigned* flag) {
   constexpr int kDT = D / 16, kF4 = kQT * D / 4;
-  const int tid = threadIdx.x, BH = a.B * a.H, ntile = a.ntile, nkb = a.nkb;
+  const int tid = threadIdx.x, BH = a.nbh, ntile = a.ntile, nkb = a.nkb;
   // Key blocks whose partials the chunk needs: all, or (causal) those holding a key <= its last
   // query.
   const int need = a.causal ? min(nkb - 1, min(a.S - 1, j1 * kQT - 1) / a.kkeys) + 1 : nkb;
@@ -1327,7 +1331,7 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
   }
   __syncthreads();
   if (*flag == 0u) return;
-  const int b = bh / a.H, h = bh % a.H, S = a.S;
+  const int b = (a.bh0 + bh) / a.H, h = (a.bh0 + bh) % a.H, S = a.S;
   const int64_t slot = static_cast<int64_t>(BH) * ntile * (kQT * D);
   const int64_t row_stride = static_cast<int64_t>(3) * a.H * D;
   float* const dq_bh =
@@ -1388,7 +1392,7 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
 template <int D>
 __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, unsigned* flag) {
   int bh, j0;
-  if (!sum_target(a.plan, x, m, a.B * a.H, a.causal, &bh, &j0)) return;
+  if (!sum_target(a.plan, x, m, a.nbh, a.causal, &bh, &j0)) return;
   bwd_sum_range<D, kSumTiles>(a, bh, j0, min(a.ntile, j0 + kSumTiles), flag);
 }
 
@@ -1420,7 +1424,7 @@ bwd_split_kernel(BwdArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, lo = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
-  const int BH = a.B * a.H, S = a.S;
+  const int BH = a.nbh, S = a.S;  // (b, h) local to this launch's chunk
   const int id = static_cast<int>(blockIdx.x);
   if (a.arrive != nullptr && id == 0 && tid == 0) *a.epoch_slot = a.epoch;  // for step 3
   if (a.arrive != nullptr && id >= a.nkb * BH) {
@@ -1446,7 +1450,8 @@ bwd_split_kernel(BwdArgs a) {
   const int item = a.causal ? id : xcd_remap(id, a.nkb * BH);
   const int bh = a.causal ? item % BH : item / a.nkb;
   const int kb = a.causal ? item / BH : item % a.nkb;
-  const int b = bh / a.H, h = bh % a.H;
+  const int bhg = a.bh0 + bh;  // the (b, h) itself
+  const int b = bhg / a.H, h = bhg % a.H;
   const int k0 = kb * kKeys;
   const int kw0 = k0 + 16 * KG * w;  // the wave's first key (KG groups of 16)
   const int key = kw0 + lo;          // this lane's key in group 0 (group c: + 16 c)
@@ -1458,7 +1463,7 @@ bwd_split_kernel(BwdArgs a) {
   const float* vp = a.v.p + b * a.v.sb + h * a.v.sh;
   const float* gp = a.d_o.p + b * a.d_o.sb + h * a.d_o.sh;
   const float* op = a.o + (static_cast<int64_t>(b) * S * a.H + h) * D;
-  const float* lp = a.lse + static_cast<int64_t>(bh) * S;
+  const float* lp = a.lse + static_cast<int64_t>(bhg) * S;
   const unsigned q_ss4 = static_cast<unsigned>(a.q.ss) * 4u;
   const unsigned g_ss4 = static_cast<unsigned>(a.d_o.ss) * 4u;
   const unsigned o_ss4 = static_cast<unsigned>(a.H) * D * 4u;
@@ -1731,15 +1736,16 @@ bwd_split_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------------------------
 template <int D>
 __device__ __forceinline__ void dq_tile(const float* __restrict__ part, float* __restrict__ dqkv,
-                                        int B, int H, int S, int nkb, int ntile, float scale,
-                                        int causal, int bh, int j, float* tile, int kkeys) {
+                                        int nbh, int bh0, int H, int S, int nkb, int ntile,
+                                        float scale, int causal, int bh, int j, float* tile,
+                                        int kkeys) {
   constexpr int kDT = D / 16, kPitch = D + 4;  // pitch: conflict-free fragment writes
   constexpr int kF4 = kQT * D / 4;             // float4s per tile
   const int tid = threadIdx.x;
-  const int b = bh / H, h = bh % H, q0 = j * kQT;
+  const int b = (bh0 + bh) / H, h = (bh0 + bh) % H, q0 = j * kQT;
   // Contributors: causal, the key blocks holding a key <= the tile's last query.
   const int cnt = causal ? min(nkb - 1, min(S - 1, q0 + kQT - 1) / kkeys) + 1 : nkb;
-  const int64_t slot = static_cast<int64_t>(B) * H * ntile * (kQT * D);
+  const int64_t slot = static_cast<int64_t>(nbh) * ntile * (kQT * D);
   const float* src = part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D);
 #pragma unroll
   for (int i = tid; i < kF4; i += kThreads) {
@@ -1784,21 +1790,21 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
                                                      unsigned long long* __restrict__ done,
                                                      unsigned long long* __restrict__ arrive,
                                                      const unsigned long long* __restrict__ epoch,
-                                                     float* __restrict__ dqkv, int B, int H,
-                                                     int S, int nkb, int ntile, float scale,
-                                                     int causal, int kkeys) {
+                                                     float* __restrict__ dqkv, int nbh, int bh0,
+                                                     int H, int S, int nkb, int ntile,
+                                                     float scale, int causal, int kkeys) {
   __shared__ __attribute__((aligned(16))) float tile[kQT * (D + 4)];
   __shared__ int todo[kThreads];
   __shared__ int ntodo;
-  const int tot = B * H * ntile;
+  const int tot = nbh * ntile;  // this launch's (b, h) chunk
   if (done == nullptr) {
     // Non-causal: the tiles of a (b, h) on the XCD that ran its key blocks in step 2 (the same
     // XCD-major split of the grid), the (b, h) written last first, whose partials are likeliest
     // still cached.
     int it = static_cast<int>(blockIdx.x);
     if (!causal && it < (tot & ~7)) it = (it & 7) * (tot >> 3) + ((tot >> 3) - 1 - (it >> 3));
-    dq_tile<D>(part, dqkv, B, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile, tile,
-               kkeys);
+    dq_tile<D>(part, dqkv, nbh, bh0, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile,
+               tile, kkeys);
     return;
   }
   const int tid = threadIdx.x;
@@ -1810,7 +1816,7 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
     if (done[first + tid] != *epoch) todo[atomicAdd(&ntodo, 1)] = first + tid;
     done[first + tid] = 0ull;
   }
-  const int nslot = B * H * nkb;
+  const int nslot = nbh * nkb;
   const int per_slot = (nslot + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
   const int slot0 = static_cast<int>(blockIdx.x) * per_slot;
   if (tid < min(per_slot, nslot - slot0)) arrive[slot0 + tid] = 0ull;
@@ -1818,8 +1824,8 @@ __global__ void __launch_bounds__(kThreads) dq_kernel(const float* __restrict__ 
   const int k = ntodo;
   for (int i = 0; i < k; ++i) {
     const int it = todo[i];
-    dq_tile<D>(part, dqkv, B, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile, tile,
-               kkeys);
+    dq_tile<D>(part, dqkv, nbh, bh0, H, S, nkb, ntile, scale, causal, it / ntile, it % ntile,
+               tile, kkeys);
     __syncthreads();  // the LDS tile is reused
   }
 }
@@ -1909,27 +1915,38 @@ int bwd_split_keys(int64_t b, int64_t h, int64_t s, int d, int causal) {
   if (d != 64 || causal || s < 512) return kBwdKeys;
   return (s + 2 * kBwdKeys - 1) / (2 * kBwdKeys) * b * h >= 512 ? 2 * kBwdKeys : kBwdKeys;
 }
-bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal) {
+namespace {
+// The schedule of a launch over nbh (b, h) pairs with key blocks of `keys` keys (a chunk's keys
+// come from the whole launch's pair count: every chunk has the whole's arithmetic).
+bool step2_sums_of(int64_t nbh, int64_t s, int d, int causal, int keys) {
   if (g_step2_sums.load(std::memory_order_relaxed) == 0) return false;
   // The range check keeps b h s (hence every count below) inside int32.
-  const int keys = bwd_split_keys(b, h, s, d, causal);
   const int nkb = static_cast<int>((s + keys - 1) / keys);
   const int ntile = static_cast<int>((s + kQT - 1) / kQT);
-  return sum_plan(static_cast<int>(b * h), nkb, ntile, d, causal).per > 0;
+  return sum_plan(static_cast<int>(nbh), nkb, ntile, d, causal).per > 0;
 }
-int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
-  if (causal || !bwd_step2_sums(b, h, s, d, causal)) return 0;
-  const int keys = bwd_split_keys(b, h, s, d, causal);
+int64_t sum_blocks_of(int64_t nbh, int64_t s, int d, int causal, int keys) {
+  if (causal || !step2_sums_of(nbh, s, d, causal, keys)) return 0;
   const int nkb = static_cast<int>((s + keys - 1) / keys);
   const int ntile = static_cast<int>((s + kQT - 1) / kQT);
-  const SumPlan p = sum_plan(static_cast<int>(b * h), nkb, ntile, d, causal);
+  const SumPlan p = sum_plan(static_cast<int>(nbh), nkb, ntile, d, causal);
   return int64_t{8} * p.per * p.nchunk;
 }
-int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal) {
-  const int64_t tiles = bwd_dq_blocks(b, h, s);
-  if (!bwd_step2_sums(b, h, s, d, causal)) return tiles;
+int64_t dq_grid_of(int64_t nbh, int64_t s, int d, int causal, int keys) {
+  const int64_t tiles = bwd_dq_blocks(1, nbh, s);
+  if (!step2_sums_of(nbh, s, d, causal, keys)) return tiles;
   const int64_t g = std::max<int64_t>(256, (tiles + kThreads - 1) / kThreads);
   return std::min(tiles, g);
+}
+}  // namespace
+bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  return step2_sums_of(b * h, s, d, causal, bwd_split_keys(b, h, s, d, causal));
+}
+int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  return sum_blocks_of(b * h, s, d, causal, bwd_split_keys(b, h, s, d, causal));
+}
+int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal) {
+  return dq_grid_of(b * h, s, d, causal, bwd_split_keys(b, h, s, d, causal));
 }
 
 
@@ -1959,22 +1976,25 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
                     const float* dsum, float* dqkv, float* part, unsigned long long* arrive,
                     unsigned long long* done, unsigned long long* epoch_slot,
                     unsigned long long epoch, int* turn, int* ctrl, int b, int h, int s, int d,
-                    float scale, int causal, void* stream) {
+                    float scale, int causal, int bh0, int nbh, void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
   const bool split = part != nullptr;
+  // The split path's grid is that of the chunk (nbh pairs) with the whole's key blocks; the
+  // turn path covers all pairs.
+  if (!split || d > 64) bh0 = 0, nbh = b * h;
   const int kkeys = split && d <= 64 ? bwd_split_keys(b, h, s, d, causal) : kBwdKeys;
   nkb = (s + kkeys - 1) / kkeys;
   const int stagger = !split && !causal && nkb <= kStaggerMaxBlocks ? 1 : 0;
-  const int64_t nsum = split ? bwd_sum_blocks(b, h, s, d, causal) : 0;
-  const int64_t nblk = int64_t{nkb} * b * h;
+  const int64_t nsum = split ? sum_blocks_of(nbh, s, d, causal, kkeys) : 0;
+  const int64_t nblk = int64_t{nkb} * nbh;
   const int64_t nmain = (nblk + 7) & ~int64_t{7};
-  if (!split || !bwd_step2_sums(b, h, s, d, causal)) {
+  if (!split || !step2_sums_of(nbh, s, d, causal, kkeys)) {
     arrive = nullptr, done = nullptr, epoch_slot = nullptr;
   }
-  const SumPlan plan = sum_plan(b * h, nkb, ntile, d, causal);
+  const SumPlan plan = sum_plan(nbh, nkb, ntile, d, causal);
   BwdArgs a{q,    k,     v,    d_o,  o,    lse,   dsum,       dqkv,  part,
             arrive, done, epoch_slot, epoch, static_cast<int>(nmain), plan, turn, ctrl, b, h, s,
-            nkb,  ntile, scale, causal, stagger, kkeys};
+            nkb,  ntile, scale, causal, stagger, kkeys, bh0, nbh};
   void* args[] = {&a};
   if (split && d <= 64) {
     const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32, 1>)
@@ -2030,18 +2050,19 @@ int static_scratch(void* stream, void** out) {
 
 int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long long* arrive,
                   const unsigned long long* epoch_slot, float* dqkv, int b, int h, int s, int d,
-                  float scale, int causal, void* stream) {
+                  float scale, int causal, int bh0, int nbh, void* stream) {
+  if (d > 64) bh0 = 0, nbh = b * h;  // (the split path at d 128 is not chunked)
   int kkeys = bwd_split_keys(b, h, s, d, causal);
   int nkb = (s + kkeys - 1) / kkeys, ntile = (s + kQT - 1) / kQT;
-  if (!bwd_step2_sums(b, h, s, d, causal)) {
+  if (!step2_sums_of(nbh, s, d, causal, kkeys)) {
     done = nullptr, arrive = nullptr, epoch_slot = nullptr;
   }
-  void* args[] = {&part,  &done, &arrive, &epoch_slot, &dqkv,  &b,
-                  &h,     &s,    &nkb,    &ntile,      &scale, &causal, &kkeys};
+  void* args[] = {&part, &done, &arrive, &epoch_slot, &dqkv,  &nbh,    &bh0,
+                  &h,    &s,    &nkb,    &ntile,      &scale, &causal, &kkeys};
   const void* fn = d == 32    ? reinterpret_cast<const void*>(dq_kernel<32>)
                    : d == 128 ? reinterpret_cast<const void*>(dq_kernel<128>)
                               : reinterpret_cast<const void*>(dq_kernel<64>);
-  return static_cast<int>(launch(fn, bwd_dq_grid(b, h, s, d, causal), args, stream));
+  return static_cast<int>(launch(fn, dq_grid_of(nbh, s, d, causal, kkeys), args, stream));
 }
 
 }  // namespace fattn

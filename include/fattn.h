@@ -72,11 +72,15 @@ int fattn_fwd_f32(const float* q, const float* k, const float* v, float* o, floa
  *      workspace (about s * s * b * h * d / 16 bytes); they are summed in key-block order by the
  *      last workgroups of step 2 (which wait, boundedly, only for key blocks dispatched before
  *      them) or by a third kernel; no key block waits on another (the faster way);
- *   >= fattn_bwd_workspace_min_bytes (below split): "turns" -- key blocks add into dQ in place,
+ *   below that, d <= 64, in fattn_bwd_f32 and the op-level backwards: "split by chunks" when the
+ *      workspace holds the split state of enough (b, h) pairs for a chunk to fill the chip (a
+ *      chunk of c pairs needs fattn_bwd_workspace_split_bytes(1, c, s, d)) -- steps 2 and 3 run
+ *      per chunk of pairs, with the same results as the whole split, bit for bit;
+ *   >= fattn_bwd_workspace_min_bytes, otherwise: "turns" -- key blocks add into dQ in place,
  *      in key-block order, under per-query-tile turn counters; D, counters and ticket only.
- * Both are deterministic. fattn_bwd_workspace_bytes is the split size when that is at most
- * FATTN_SPLIT_MAX_BYTES, else the minimum. All three return 0 for a negative size or an
- * unsupported d. */
+ * All are deterministic. fattn_bwd_workspace_bytes is the split size when that is at most
+ * FATTN_SPLIT_MAX_BYTES, else the split of the largest worthwhile chunk within it (d <= 64),
+ * else the minimum. All three return 0 for a negative size or an unsupported d. */
 #define FATTN_SPLIT_MAX_BYTES ((size_t)4 << 30)
 size_t fattn_bwd_workspace_bytes(int64_t b, int64_t h, int64_t s, int64_t d);
 size_t fattn_bwd_workspace_min_bytes(int64_t b, int64_t h, int64_t s, int64_t d);

@@ -50,7 +50,7 @@ def test_workspace_size_is_aligned_and_monotone():
     lo = L.fattn_bwd_workspace_min_bytes(64, 6, 240, 64)
     hi = L.fattn_bwd_workspace_split_bytes(64, 6, 240, 64)
     assert n1 % 256 == 0 and lo % 256 == 0 and hi % 256 == 0
-    # minimum: D (64*6*240 f32) + turns (64*6*15 i32) + control
+    # minimum: control + D (64*6*240 f32) + turns (64*6*15 i32)
     assert lo >= 64 * 6 * 240 * 4 + 64 * 6 * 15 * 4 + 256
     # split: plus one 16 x d f32 partial per key block (4) and query tile (15) of each (b, h), a
     # u64 arrival slot per key block and a u64 done flag per query tile (both 256-byte multiples
@@ -64,10 +64,21 @@ def test_workspace_size_is_aligned_and_monotone():
     assert L.fattn_bwd_workspace_bytes(-1, 6, 240, 64) == 0
     assert L.fattn_bwd_workspace_min_bytes(-1, 6, 240, 64) == 0
     assert L.fattn_bwd_workspace_bytes(64, 6, 240, 48) == 0      # head_dim not built
-    # Past FATTN_SPLIT_MAX_BYTES (4 GiB) the default falls back to the minimum (turns).
-    assert L.fattn_bwd_workspace_split_bytes(1, 64, 16384, 64) > 4 << 30
+    # Past FATTN_SPLIT_MAX_BYTES (4 GiB), at d <= 64: the split sum of equal chunks of (b, h),
+    # each chunk's state in a workspace laid out for that many pairs (split_bytes(1, chunk, ...));
+    # at d 128 the minimum (the turn hand-over).
+    cap = 4 << 30
+    assert L.fattn_bwd_workspace_split_bytes(1, 64, 16384, 64) > cap
+    # 1 GiB of partials per pair: 3 fit, 22 chunks of 3 (the last of 1)
     assert (L.fattn_bwd_workspace_bytes(1, 64, 16384, 64)
-            == L.fattn_bwd_workspace_min_bytes(1, 64, 16384, 64))
+            == L.fattn_bwd_workspace_split_bytes(1, 3, 16384, 64))
+    assert L.fattn_bwd_workspace_split_bytes(1, 4, 16384, 64) > cap
+    # 64 MiB per pair: 63 fit, rounded to 56 (8 | chunk), so 3 chunks, made equal: 48, 48, 32
+    assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 64)
+            == L.fattn_bwd_workspace_split_bytes(1, 48, 4096, 64))
+    assert L.fattn_bwd_workspace_split_bytes(1, 64, 4096, 64) > cap
+    assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 128)
+            == L.fattn_bwd_workspace_min_bytes(8, 16, 4096, 128))
 
 
 def test_head_dim_gate_before_alignment():

@@ -755,9 +755,9 @@ def ws_layout(b, h, s, d):
     workspace_layout; the library's reported sizes pin it)."""
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     tiles, nkb = b * h * (-(-s // 16)), -(-s // 64)
-    lay = {"d": 0, "turn": up(b * h * s * 4)}
-    lay["ctrl"] = lay["turn"] + up(tiles * 4)
-    lay["part"] = lay["ctrl"] + 256
+    lay = {"ctrl": 0, "d": 256}
+    lay["turn"] = lay["d"] + up(b * h * s * 4)
+    lay["part"] = lay["turn"] + up(tiles * 4)
     lay["arrive"] = lay["part"] + up(nkb * tiles * 16 * d * 4)
     lay["done"] = lay["arrive"] + up(b * h * nkb * 8)
     lay["epoch"] = lay["done"] + up(tiles * 8)
@@ -1064,3 +1064,53 @@ def test_random_layouts(orc, cuda, seed):
         tol = max(REL_TOL, 1.5 * orc.rel_fro(floor[name], r))
         say(f"  {name}: {err:.2e} (bar {tol:.2e})")
         assert err <= tol, f"{name}: normwise error {err:.3e} > {tol:.3e}"
+
+
+# --- the split dQ sum by chunks of (b, h) (a workspace that holds some pairs' partials) ---------
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_split_by_chunks_matches_whole(cuda, causal):
+    """fattn_bwd_f32 with a workspace that holds the split partials of only some (b, h) pairs runs
+    steps 2 and 3 per chunk of pairs (causal: equal, 8 | chunk; non-causal: whole rounds of slots), where the chunks are
+    large enough to beat the turn hand-over (s 4096: 12 pairs non-causal, 48 causal): the
+    gradient equals the whole split's bit for bit (each pair's arithmetic and summation order are
+    the same), and the guard word reads 0. Non-causal b h 24 in chunks of 16 and 8; causal b h 96
+    in two of 48. A workspace whose chunks would be smaller takes the turn hand-over: causal, its
+    gradient equals the split's bit for bit too."""
+    b, h, s, d = (2, 12, 4096, 64) if not causal else (6, 16, 4096, 64)
+    pairs = 16 if not causal else 48
+    L = _lib.lib()
+    g = torch.Generator(device=cuda).manual_seed(7)
+    qkv = torch.randn(b, s, 3 * h * d, generator=g, device=cuda)
+    dout = torch.randn(b, s, h * d, generator=g, device=cuda)
+    st = _lib.arr([s * 3 * h * d, d, 3 * h * d])
+    gst = _lib.arr([s * h * d, d, h * d])
+    qp, kp, vp = (ctypes.c_void_p(qkv.data_ptr() + i * h * d * 4) for i in range(3))
+    stream = _st(qkv)
+    o = torch.empty(b, s, h * d, device=cuda)
+    lse = torch.empty(b, h, s, device=cuda)
+    _lib.check(L.fattn_fwd_f32(qp, kp, vp, _p(o), _p(lse), b, h, s, d, 0.125, int(causal), st, st,
+                               st, stream))
+
+    def backward(n):
+        ws = torch.empty(n, dtype=torch.uint8, device=cuda)
+        out = torch.full_like(qkv, float("nan"))
+        _lib.check(L.fattn_bwd_f32(qp, kp, vp, _p(o), _p(dout), _p(lse), _p(out), _p(ws), n, b, h,
+                                   s, d, 0.125, int(causal), st, st, st, gst, stream))
+        status = ctypes.c_int(-1)
+        _lib.check(L.fattn_bwd_status(_p(ws), n, b, h, s, stream, ctypes.byref(status)))
+        assert status.value == 0
+        del ws
+        return out
+
+    whole_n = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
+    whole = backward(whole_n)
+    assert torch.isfinite(whole).all()
+    n = L.fattn_bwd_workspace_split_bytes(1, pairs, s, d)
+    assert n < whole_n
+    say(f"chunks of {pairs} (b, h) causal={causal}: workspace {n >> 20} MiB of {whole_n >> 20}")
+    assert torch.equal(bits(backward(n)), bits(whole)), f"chunks of {pairs}"
+    if causal:
+        small = L.fattn_bwd_workspace_split_bytes(1, 8, s, d)   # chunks of 8: turns instead
+        say(f"workspace for 8 pairs ({small >> 20} MiB): the turn hand-over")
+        assert torch.equal(bits(backward(small)), bits(whole))

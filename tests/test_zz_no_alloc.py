@@ -1,8 +1,9 @@
 """fattn_bwd_f32_noalloc (the backward with the library's static scratch as its workspace) against
-fattn_bwd_f32 with a caller's workspace of the kind the no-alloc entry picks (split when the split
-workspace fits in FATTN_STATIC_SCRATCH_BYTES, else turns): bit-identical dQ, dK, dV on two calls
-in a row, the second on a smaller shape, causal and not, and the refusal of a shape whose minimum
-workspace exceeds the scratch (before any launch)."""
+fattn_bwd_f32 with a caller's workspace of the scratch's size, FATTN_STATIC_SCRATCH_BYTES (so the
+same way of summing dQ: the whole split when it fits, else the split by chunks of (b, h) at
+d <= 64, else turns): bit-identical dQ, dK, dV on two calls in a row, the second on a smaller
+shape, causal and not, and the refusal of a shape whose minimum workspace exceeds the scratch
+(before any launch)."""
 from __future__ import annotations
 
 import ctypes
@@ -43,8 +44,9 @@ def backward_both(b, h, s, d, causal, seed, dev):
     _lib.check(L.fattn_fwd_f32(qp, kp, vp, P(o), P(lse), b, h, s, d, scale, int(causal), st, st,
                                st, stream))
     split = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
-    n = split if split <= STATIC_SCRATCH else L.fattn_bwd_workspace_min_bytes(b, h, s, d)
-    kind = "split" if n == split else "turns"
+    n = STATIC_SCRATCH
+    kind = ("split" if split <= n else "split by chunks" if d <= 64
+            and L.fattn_bwd_workspace_split_bytes(1, 1, s, d) <= n else "turns")
     ws = torch.empty(n, dtype=torch.uint8, device=dev)
     want = torch.full_like(qkv, float("nan"))
     _lib.check(L.fattn_bwd_f32(qp, kp, vp, P(o), P(dout), P(lse), P(want), P(ws), n, b, h, s, d,
@@ -59,7 +61,8 @@ def backward_both(b, h, s, d, causal, seed, dev):
 @pytest.mark.parametrize("causal", [False, True])
 def test_noalloc_matches_workspace_entry(cuda, causal):
     # (b, h, s, d): split fits the scratch, then a smaller split shape; the config-2 shape (its
-    # split workspace exceeds the scratch: turns), then a smaller one; head_dim 32 and 128.
+    # split workspace exceeds the scratch: split by chunks), then a smaller one; head_dim 32 and
+    # 128 (the latter past the scratch: turns).
     cases = [((4, 6, 240, 64), (2, 3, 97, 64)),
              ((64, 6, 240, 64), (8, 6, 200, 64)),
              ((2, 4, 333, 32), (1, 2, 65, 32)),
@@ -90,8 +93,9 @@ def test_noalloc_refuses_what_does_not_fit(cuda):
 def test_noalloc_under_graph_capture(cuda, shape):
     """The no-alloc backward is for callers under HIP graph capture: the forward and
     fattn_bwd_f32_noalloc captured in one graph and replayed on new inputs (with eager work and
-    synchronisations between replays) equal eager fattn_bwd_f32 runs with a workspace of the kind
-    the no-alloc entry picks (config 2's shape: turns; the smaller one: split), bit for bit."""
+    synchronisations between replays) equal eager fattn_bwd_f32 runs with a workspace of the
+    scratch's size (config 2's shape: the split by chunks, several launches captured; the smaller
+    one: the whole split), bit for bit."""
     b, h, s = shape
     d = 64
     L = _lib.lib()
@@ -103,8 +107,8 @@ def test_noalloc_under_graph_capture(cuda, shape):
     st = _lib.arr([s * 3 * h * d, d, 3 * h * d])
     gst = _lib.arr([s * h * d, d, h * d])
     qp, kp, vp = (ctypes.c_void_p(qkv.data_ptr() + i * h * d * 4) for i in range(3))
-    split = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
-    n = split if split <= STATIC_SCRATCH else L.fattn_bwd_workspace_min_bytes(b, h, s, d)
+    n = STATIC_SCRATCH
+    kind = "split" if L.fattn_bwd_workspace_split_bytes(b, h, s, d) <= n else "split by chunks"
     ws = torch.empty(n, dtype=torch.uint8, device=cuda)
 
     def captured():
@@ -137,7 +141,7 @@ def test_noalloc_under_graph_capture(cuda, shape):
     with torch.cuda.graph(graph):
         captured()
     for r in range(3):
-        say(f"noalloc graph replay {r} shape {shape} ({'split' if n == split else 'turns'})")
+        say(f"noalloc graph replay {r} shape {shape} ({kind})")
         qkv.copy_(torch.randn(qkv.shape, generator=gen))
         dout.copy_(torch.randn(dout.shape, generator=gen))
         got.fill_(float("nan"))
