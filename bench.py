@@ -13,10 +13,11 @@ are timed too, as extra keys of the same line (`configs`): op-level forward and
 forward+backward, and each kernel on its own.
 
 Order of the GPU work: W warm-up + K timed steps from an idle GPU (`fwd_bwd_from_idle_ms`),
-configs 3-5 and the two head_dims, then W warm-up + K timed steps (`value`), K forwards (`fwd_ms`) and K kernel-level
-steps (`kernels_us`, `roofline`). MI355X runs at lower clocks for some tens of milliseconds after
-an idle second, so the headline steps come right after sustained work, as in a training loop; the
-from-idle figure shows what a short run on an idle GPU sees.
+configs 3-5, then W warm-up + K timed steps (`value`), K forwards (`fwd_ms`), K kernel-level
+steps (`kernels_us`, `roofline`), and last config 2 at head_dim 32 and 128. MI355X runs at
+lower clocks for some tens of milliseconds after an idle second, so the headline steps come right
+after sustained work, as in a training loop; the from-idle figure shows what a short run on an
+idle GPU sees.
 
 Prints ONE JSON line. `--gpus N` with N > 1 exits: this build runs on one GPU.
 
@@ -292,7 +293,7 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
     kernel-level steps (whose average step-2 duration is `kernels_us.bwd_main`), and the first
     K steps from idle. Configs 3-5 run the same kernel names, so the dispatches are split into
     steps (a step starts at a forward launch) and config 2's steps picked by the forward's name
-    and grid; the headline's are those after the last step of another config."""
+    and grid; the headline's are the run of them after configs 3-5."""
     rows = []
     with open(trace_csv, newline="") as f:
         for r in csv.DictReader(f):
@@ -312,17 +313,29 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
             steps_seq.append([])
         steps_seq[-1].append((name, wgs, us))
     is_main = [st[0][0] == main_fwd[0] and st[0][1] == main_fwd[1] for st in steps_seq]
-    other = [i for i, m in enumerate(is_main) if not m]
-    if other:
-        first = other[-1] + 1
-        idle = steps_seq[warmup:warmup + steps] if all(is_main[:warmup + steps]) else []
-    else:
+    # Runs of consecutive config-2 steps: the idle run opens the trace (unless --no-extra, when
+    # the trace is one run); the headline's is the first run after another config's steps that
+    # holds the W warm-up, K timed, K forward and K kernel-level steps.
+    runs, start = [], None
+    for i, m in enumerate(is_main + [False]):
+        if m and start is None:
+            start = i
+        elif not m and start is not None:
+            runs.append((start, i))
+            start = None
+    need = warmup + 3 * steps
+    if len(runs) == 1 and runs[0][0] == 0:
         first, idle = warmup + steps, steps_seq[warmup:warmup + steps]
+    else:
+        idle = (steps_seq[warmup:warmup + steps]
+                if runs and runs[0][0] == 0 and runs[0][1] >= warmup + steps else [])
+        later = [r for r in runs if r[0] > 0 and r[1] - r[0] >= need]
+        first = later[0][0] if later else len(steps_seq)
     timed = steps_seq[first + warmup:first + warmup + steps]
     kern = steps_seq[first + warmup + 2 * steps:first + warmup + 3 * steps]
     if len(timed) < steps or len(kern) < steps:
-        print(f"bench.py: the trace holds {len(steps_seq) - first} config-2 steps after the "
-              f"other configs; expected at least {warmup + 3 * steps}", file=sys.stderr)
+        print(f"bench.py: the trace holds no run of {need} config-2 steps after the other "
+              "configs", file=sys.stderr)
         return 1
 
     def table(title, seq):
@@ -457,12 +470,6 @@ def main() -> int:
             extra[f"config{cfg}"] = time_extra(torch, xw, max(args.extra_steps, 1), 100)
             log(f"bench: {CONFIGS[cfg][0]}: {json.dumps(extra[f'config{cfg}'])}")
             del xw
-        # The other head dims the kernels are built for, at the headline's shape.
-        for d in (32, 128):
-            xw = Workload(torch, L, _lib, dev, 2, d=d)
-            extra[f"config2_d{d}"] = time_extra(torch, xw, max(args.extra_steps, 1), 100)
-            log(f"bench: config 2 at d {d}: {json.dumps(extra[f'config2_d{d}'])}")
-            del xw
         torch.cuda.synchronize()
 
     for _ in range(max(args.warmup, 1)):
@@ -492,6 +499,17 @@ def main() -> int:
     dq_us = kus.get("bwd_dq", 0.0)
     log(f"bench: kernels fwd {fwd_us:.1f} us, prep {prep_us:.1f} us, bwd main {main_us:.1f} us, "
         f"dq sum {dq_us:.1f} us ({'split' if w.split else 'turns'}); step {kus['step']:.1f} us")
+
+    if not args.no_extra:
+        # The other head dims the kernels are built for, at the headline's shape: after the
+        # headline (right before it, the heavier head_dim 128 work left the next 25 steps 4 %
+        # slower in a kernel trace than the same kernels a few ms later).
+        for d in (32, 128):
+            xw = Workload(torch, L, _lib, dev, 2, d=d)
+            extra[f"config2_d{d}"] = time_extra(torch, xw, max(args.extra_steps, 1), 100)
+            log(f"bench: config 2 at d {d}: {json.dumps(extra[f'config2_d{d}'])}")
+            del xw
+        torch.cuda.synchronize()
 
     f_fwd, f_bwd = w.flops()
     fwd_tflops = f_fwd / (fwd_ms * 1e-3) / 1e12
@@ -530,9 +548,9 @@ def main() -> int:
         "fwd_bwd_from_idle_first5_ms": round(statistics.mean(cold_steps[:n5]), 5),
         "fwd_bwd_from_idle_last5_ms": round(statistics.mean(cold_steps[-n5:]), 5),
         "sequence": ("W warm-up + K timed steps from idle (fwd_bwd_from_idle_ms), "
-                     + ("configs 3-5 and config 2 at d 32 / 128 timed (configs), "
-                        if extra else "")
-                     + "W warm-up + K timed steps (value), K forwards, K kernel-level steps"),
+                     + ("configs 3-5 timed (configs), " if extra else "")
+                     + "W warm-up + K timed steps (value), K forwards, K kernel-level steps"
+                     + (", config 2 at d 32 / 128 timed (configs)" if extra else "")),
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_bwd_tflops": round(total_tflops, 3),
         "frac_fp32_peak": round(total_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
