@@ -41,6 +41,10 @@ Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d) {
   return w;
 }
 
+// The split step 2's workgroup slots on gfx950 (256 CUs): 3 per CU with 64-key blocks, 2 with
+// 128-key blocks.
+int64_t split_slots(int keys) { return (keys > kBwdKeys ? 2 : 3) * int64_t{256}; }
+
 // The (b, h) pairs per chunk of the split dQ sum that a workspace of ws_bytes holds: b h when it
 // holds the whole split; else, at d <= 64, from the most pairs whose split partials, arrival
 // slots and done flags fit:
@@ -66,10 +70,8 @@ int64_t split_chunk(int64_t b, int64_t h, int64_t s, int64_t d, size_t ws_bytes,
     }
   }
   if (!causal) {
-    // Key blocks per pair, and the slots they fill: 128-key blocks run 2 workgroups per CU,
-    // 64-key blocks 3 (256 CUs on gfx950).
     const int keys = bwd_split_keys(b, h, s, static_cast<int>(d), 0);
-    const int64_t nkb = (s + keys - 1) / keys, slots = (keys > kBwdKeys ? 2 : 3) * int64_t{256};
+    const int64_t nkb = (s + keys - 1) / keys, slots = split_slots(keys);
     const int64_t quantum = slots / std::gcd(slots, nkb);
     if (lo >= quantum) lo -= lo % quantum;
     return lo == 0 || lo < min_pairs ? 0 : lo;
@@ -87,14 +89,14 @@ int64_t split_chunk(int64_t b, int64_t h, int64_t s, int64_t d, size_t ws_bytes,
 // The fewest (b, h) pairs a chunk should hold. A chunk is one launch of step 2: with too few key
 // blocks it runs at a fraction of the chip, so chunks of fewer pairs than this lose to the turn
 // hand-over over all pairs (measured: b 4 h 16 s 8192 causal, chunks of 8 pairs 15.1 ms against
-// 13.8 with turns). Non-causal: the chunk's key blocks fill the chip's workgroup slots (3 per CU,
-// 256 CUs on gfx950) at least once. Causal: the key blocks' walks shrink with the block index, so
-// the slots' average work must be at least twice the longest walk (block 0's, all query tiles):
-// four times the slots in key blocks.
-int64_t min_chunk_pairs(int64_t s, bool causal) {
-  constexpr int64_t kSlots = 3 * 256;
-  const int64_t nkb = (s + kBwdKeys - 1) / kBwdKeys;
-  const int64_t blocks = causal ? 4 * kSlots : kSlots;
+// 13.8 with turns). Non-causal: the chunk's key blocks fill the chip's workgroup slots at least
+// once. Causal: the key blocks' walks shrink with the block index, so the slots' average work must
+// be at least twice the longest walk (block 0's, all query tiles): four times the slots in key
+// blocks.
+int64_t min_chunk_pairs(int64_t b, int64_t h, int64_t s, int64_t d, bool causal) {
+  const int keys = bwd_split_keys(b, h, s, static_cast<int>(d), causal ? 1 : 0);
+  const int64_t nkb = (s + keys - 1) / keys;
+  const int64_t blocks = (causal ? 4 : 1) * split_slots(keys);
   return (blocks + nkb - 1) / nkb;
 }
 
@@ -105,7 +107,7 @@ size_t workspace_within(int64_t b, int64_t h, int64_t s, int64_t d, size_t limit
   const Workspace l = workspace_layout(b, h, s, d);
   if (l.bytes_split <= limit) return l.bytes_split;
   // (sized with the causal rule, whose chunk sizes the non-causal rule's fit too)
-  const int64_t c = split_chunk(b, h, s, d, limit, min_chunk_pairs(s, false), true);
+  const int64_t c = split_chunk(b, h, s, d, limit, min_chunk_pairs(b, h, s, d, false), true);
   return c > 0 ? workspace_layout(1, c, s, d).bytes_split : l.bytes_min;
 }
 
@@ -371,8 +373,8 @@ int run_backward(const char* who, View q, View k, View v, const float* o, View d
   if (int rc = check_range(who, b, h, s, d)) return rc;
   int64_t chunk = 0;
   if (ws) {
-    chunk = fattn::split_chunk(b, h, s, d, ws_bytes, fattn::min_chunk_pairs(s, causal != 0),
-                               causal != 0);
+    chunk = fattn::split_chunk(b, h, s, d, ws_bytes,
+                               fattn::min_chunk_pairs(b, h, s, d, causal != 0), causal != 0);
     if (chunk == 0 && ws_bytes < fattn::workspace_layout(b, h, s, d).bytes_min) {
       chunk = fattn::split_chunk(b, h, s, d, ws_bytes, 1, causal != 0);
     }

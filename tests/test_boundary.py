@@ -69,10 +69,15 @@ def test_workspace_size_is_aligned_and_monotone():
     # at d 128 the minimum (the turn hand-over).
     cap = 4 << 30
     assert L.fattn_bwd_workspace_split_bytes(1, 64, 16384, 64) > cap
-    # 1 GiB of partials per pair: 3 fit, 22 chunks of 3 (the last of 1)
-    assert (L.fattn_bwd_workspace_bytes(1, 64, 16384, 64)
-            == L.fattn_bwd_workspace_split_bytes(1, 3, 16384, 64))
+    # 1 GiB of partials per pair: 3 fit, but their 3 x 128 key blocks (of 128 keys) fill less than
+    # one round of the 512 workgroup slots: the minimum (turns)
+    assert L.fattn_bwd_workspace_split_bytes(1, 3, 16384, 64) <= cap
     assert L.fattn_bwd_workspace_split_bytes(1, 4, 16384, 64) > cap
+    assert (L.fattn_bwd_workspace_bytes(1, 64, 16384, 64)
+            == L.fattn_bwd_workspace_min_bytes(1, 64, 16384, 64))
+    # 256 MiB per pair: 15 fit, 8 (a multiple of 8) fill one round: chunks of 8
+    assert (L.fattn_bwd_workspace_bytes(4, 16, 8192, 64)
+            == L.fattn_bwd_workspace_split_bytes(1, 8, 8192, 64))
     # 64 MiB per pair: 63 fit, rounded to 56 (8 | chunk), so 3 chunks, made equal: 48, 48, 32
     assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 64)
             == L.fattn_bwd_workspace_split_bytes(1, 48, 4096, 64))
