@@ -90,7 +90,8 @@ struct SumPlan {
 };
 __host__ __device__ inline SumPlan sum_plan(int BH, int nkb, int ntile, int d, int causal) {
   SumPlan p{0, (ntile + kSumTiles - 1) / kSumTiles};
-  if (d > 64 || nkb > kSumMaxBlocks || BH <= 0) return p;
+  // (At d 128 the split kernel has the non-causal tail sums only.)
+  if ((d > 64 && causal) || nkb > kSumMaxBlocks || BH <= 0) return p;
   if (causal) {
     p.per = BH % 8 == 0 ? BH / 8 : 0;
   } else {

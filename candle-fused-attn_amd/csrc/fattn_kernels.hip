@@ -795,6 +795,9 @@ __device__ __forceinline__ bool wait_turn(int* p, int want, int* guard) {
 
 // Occupancy target: BWD_WAVES waves per SIMD (the kernel is latency-bound: with fewer, the
 // matrix cores idle behind barriers), 2 at D 128 (its registers do not fit 3).
+template <int D>
+__device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, unsigned* flag);
+
 template <bool kSplit, int D>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArgs a) {
@@ -817,6 +820,7 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   __shared__ __attribute__((aligned(16))) float sL[2][kQT];
   __shared__ __attribute__((aligned(16))) float sD[2][kQT];
   __shared__ int s_item;
+  __shared__ unsigned s_flag;  // a dQ sum's poll result (split, non-causal)
 
   const int tid = threadIdx.x, lane = tid & 63, lo = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
@@ -824,9 +828,15 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   int item;
   if (kSplit) {
     // No workgroup waits on another: the workgroup index is the item. Non-causal: the key blocks
-    // of one (b, h) on one XCD (they read the same Q and dO tiles at about the same time).
+    // of one (b, h) on one XCD (they read the same Q and dO tiles at about the same time), and
+    // the dQ sums of step 2's tail in the workgroups appended to the grid (as bwd_split_kernel's).
     // Causal: round-robin over the XCDs, which spreads the expensive low blocks evenly.
-    const int n = static_cast<int>(gridDim.x), id = static_cast<int>(blockIdx.x);
+    const int n = a.nkb * BH, id = static_cast<int>(blockIdx.x);
+    if (a.arrive != nullptr && id == 0 && tid == 0) *a.epoch_slot = a.epoch;  // for step 3
+    if (a.arrive != nullptr && id >= n) {
+      if (id >= a.n_main) bwd_sum_tiles<D>(a, id & 7, (id - a.n_main) >> 3, &s_flag);
+      return;
+    }
     item = a.causal ? id : xcd_remap(id, n);
     // No turn waits here: the guard word reads 0 (step 1, which clears it for the turn mode, does
     // not run for the split mode).
@@ -1229,6 +1239,18 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   // Drain: the tiles still in the pipeline, in order.
   if (kSplit) {
     if (p1_q0 >= 0) store_part(p1_q0, p1);
+    if (a.arrive != nullptr) {
+      // Every partial of this key block is stored once the stores of every wave have completed:
+      // record its arrival, with the XCD it runs on (as bwd_split_kernel does).
+      wait_stores();
+      __syncthreads();
+      if (tid == 0) {
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        __hip_atomic_store(a.arrive + static_cast<int64_t>(bh) * a.nkb + kb, a.epoch | (xcc & 7u),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   } else if (p2_q0 >= 0) {
     store_sums(p2_q0, p2_pos, p2_cnt, p2, p2s);
     wait_stores();
@@ -1336,11 +1358,10 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
   const int64_t row_stride = static_cast<int64_t>(3) * a.H * D;
   float* const dq_bh =
       a.dqkv + static_cast<int64_t>(b) * S * row_stride + static_cast<int64_t>(h) * D;
-  // Thread i sums float4 i of each of the tiles, four key blocks at a time: the loads of all the
-  // tiles for those key blocks are issued together, then added in key-block order.
-  static_assert(kF4 <= kThreads, "one float4 of each tile per thread");
-  const int i = tid;
-  if (i < kF4) {
+  // Thread i sums float4 i (and i + kThreads, ... at D 128) of each of the tiles, four key blocks
+  // at a time: the loads of all the tiles for those key blocks are issued together, then added in
+  // key-block order.
+  for (int i = tid; i < kF4; i += kThreads) {
     int cnt[NT];
     const float* src[NT];
     f4 acc[NT];
@@ -2012,6 +2033,8 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   } else {
     fn = reinterpret_cast<const void*>(bwd_kernel<false, 64>);
   }
+  // (Split at 128: the key blocks, then the workgroups of the tail sums, as above.)
+  if (split) return static_cast<int>(launch(fn, nsum ? nmain + nsum : nblk, args, stream));
   return static_cast<int>(launch(fn, bwd_main_blocks(b, h, s), args, stream));
 }
 

@@ -341,8 +341,9 @@ def test_step2_dq_sum_schedule(causal):
     grid, no target lies past b h (the case a rounded-up per-XCD count once produced: nkb = 1, b h
     not a multiple of 8, e.g. h 17 s 50), no tile is summed twice, and exactly the (b, h)s the
     schedule's definition puts wholly on one XCD are summed, every one of their tiles.
-    Non-causal, the units are workgroups appended to the grid, ceil(ntile / 3) per (b, h); causal,
-    every key block's own workgroup sums its diagonal tiles (none appended)."""
+    Non-causal, the units are workgroups appended to the grid, ceil(ntile / 3) per (b, h) (every
+    head_dim); causal, every key block's own workgroup sums its diagonal tiles (none appended; d 64
+    and below: step 3 sums them at d 128)."""
     n = 0
     for s in (1, 16, 50, 64, 65, 100, 128, 200, 240, 333, 511, 512, 600, 1024, 2048):
         for bh in list(range(1, 41)) + [48, 64, 96, 128, 192, 256, 384]:
@@ -351,7 +352,8 @@ def test_step2_dq_sum_schedule(causal):
                 keys = expected_keys(bh, s, d, causal)
                 assert a["keys"] == keys, (s, bh, d, a)
                 ntile, nkb = -(-s // 16), -(-s // keys)
-                want_bh = expected_sum_bh(bh, s, causal, keys) if d <= 64 else 0
+                # d 128: the non-causal tail sums only
+                want_bh = expected_sum_bh(bh, s, causal, keys) if d <= 64 or not causal else 0
                 assert a["bad"] == 0 and a["twice"] == 0, (s, bh, d, a)
                 assert a["covered"] == want_bh * ntile, (s, bh, d, a, want_bh)
                 if causal:

@@ -625,7 +625,7 @@ def test_split_and_turns_agree(orc, cuda, causal):
 
 
 @pytest.mark.parametrize("d,h,s", [(64, 9, 240), (64, 9, 100), (64, 17, 50), (32, 9, 240),
-                                   (32, 17, 100)])
+                                   (32, 17, 100), (128, 9, 240), (128, 17, 100)])
 def test_dq_sums_in_step2_match_step3(orc, cuda, d, h, s):
     """Non-causal split backward: the last workgroups of step 2 sum the dQ tiles of the (b, h)s
     whose key blocks an XCD ran (with workgroups dealt to the XCDs round robin: heads 0-7, or 0-15
