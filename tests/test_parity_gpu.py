@@ -1028,6 +1028,26 @@ def layout_of(kind, vals, rng, cuda):
     return v.detach().requires_grad_(True)
 
 
+def check_against_oracle(orc, got, vals, scale, causal):
+    """Output and gradients against the fp64 oracle at the bar of the other parity tests."""
+    qn, kn, vn, wn = vals
+    ref, floor = {}, {}
+    for dtype, dst in ((np.float64, ref), (np.float32, floor)):
+        o, l_ = orc.forward(qn, kn, vn, scale, causal, dtype)
+        dq, dk, dv = orc.backward(qn, kn, vn, o, l_, wn, scale, causal, dtype)
+        dst.update(o=o, dq=dq, dk=dk, dv=dv)
+    for name in ("o", "dq", "dk", "dv"):
+        r = np.asarray(ref[name], dtype=np.float64)
+        if not np.any(r):
+            dev = float(np.abs(got[name]).max())
+            assert dev <= BAND, f"{name} (exactly zero in fp64) max deviation {dev:.3e}"
+            continue
+        err = orc.rel_fro(got[name], r)
+        tol = max(REL_TOL, 1.5 * orc.rel_fro(floor[name], r))
+        say(f"  {name}: {err:.2e} (bar {tol:.2e})")
+        assert err <= tol, f"{name}: normwise error {err:.3e} > {tol:.3e}"
+
+
 @pytest.mark.parametrize("seed", range(20))
 def test_random_layouts(orc, cuda, seed):
     """fused_attention on q, k, v and an output gradient in layouts drawn at random (each operand
@@ -1048,22 +1068,38 @@ def test_random_layouts(orc, cuda, seed):
     torch.cuda.synchronize()
     got = {"o": out.detach().cpu().numpy(), "dq": q.grad.cpu().numpy(),
            "dk": k.grad.cpu().numpy(), "dv": v.grad.cpu().numpy()}
-    qn, kn, vn, wn = vals
-    ref, floor = {}, {}
-    for dtype, dst in ((np.float64, ref), (np.float32, floor)):
-        o, l_ = orc.forward(qn, kn, vn, scale, causal, dtype)
-        dq, dk, dv = orc.backward(qn, kn, vn, o, l_, wn, scale, causal, dtype)
-        dst.update(o=o, dq=dq, dk=dk, dv=dv)
-    for name in ("o", "dq", "dk", "dv"):
-        r = np.asarray(ref[name], dtype=np.float64)
-        if not np.any(r):
-            dev = float(np.abs(got[name]).max())
-            assert dev <= BAND, f"{name} (exactly zero in fp64) max deviation {dev:.3e}"
-            continue
-        err = orc.rel_fro(got[name], r)
-        tol = max(REL_TOL, 1.5 * orc.rel_fro(floor[name], r))
-        say(f"  {name}: {err:.2e} (bar {tol:.2e})")
-        assert err <= tol, f"{name}: normwise error {err:.3e} > {tol:.3e}"
+    check_against_oracle(orc, got, vals, scale, causal)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_random_qkv_cases(orc, cuda, seed):
+    """fused_attention_qkv at random b (1-4), h (1-8), s (1-400), head_dim (32, 64, 128), mask,
+    scale (either sign) and dQ-sum mode (auto, split, turns): the output and the three slices of
+    the qkv gradient against the fp64 oracle (src/lib.rs:241-299; the operator, src/lib.rs:506-580)."""
+    rng = np.random.default_rng(50000 + seed)
+    b, h = int(rng.integers(1, 5)), int(rng.integers(1, 9))
+    s, d = int(rng.integers(1, 401)), int(rng.choice([32, 64, 128]))
+    causal = bool(rng.integers(0, 2))
+    scale = float(rng.choice([-1.0, 1.0]) * rng.uniform(0.02, 0.4))
+    mode = str(rng.choice(["auto", "split", "turns"]))
+    say(f"seed {seed}: b {b} h {h} s {s} d {d} causal={causal} scale {scale:.4f} dq_sum {mode}")
+    x = rng.standard_normal((b, s, 3 * h * d)).astype(np.float32)
+    wq = rng.standard_normal((b, s, h * d)).astype(np.float32)
+    prev = cfa.set_dq_sum(mode)
+    try:
+        xt = torch.from_numpy(x).to(cuda).requires_grad_(True)
+        out = cfa.fused_attention_qkv(xt, h, scale, causal)
+        out.backward(torch.from_numpy(wq).to(cuda))
+        torch.cuda.synchronize()
+    finally:
+        cfa.set_dq_sum(prev)
+    g = xt.grad.cpu().numpy().reshape(b, s, 3, h, d).transpose(2, 0, 3, 1, 4)
+    got = {"o": out.detach().cpu().numpy().reshape(b, s, h, d).transpose(0, 2, 1, 3),
+           "dq": g[0], "dk": g[1], "dv": g[2]}
+    x5 = x.reshape(b, s, 3, h, d).transpose(2, 0, 3, 1, 4)
+    vals = [np.ascontiguousarray(x5[i]) for i in range(3)]
+    vals.append(np.ascontiguousarray(wq.reshape(b, s, h, d).transpose(0, 2, 1, 3)))
+    check_against_oracle(orc, got, vals, scale, causal)
 
 
 # --- the split dQ sum by chunks of (b, h) (a workspace that holds some pairs' partials) ---------
