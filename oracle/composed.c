@@ -8,7 +8,9 @@
  *   - oracle_backward_f32   = composed_backward     (src/lib.rs:269-299)
  *   - oracle_forward_f64 / oracle_backward_f64: the same formulas in double precision, the
  *     fp64 recompute every result is scored against (bench/compare.py:506-536 scores against
- *     torch fp64 autograd of the same composition).
+ *     torch fp64 autograd of the same composition);
+ *   - oracle_rows_f32 / oracle_rows_f64: the same, at sampled rows of one slice, for sequences
+ *     too long for [s][s] buffers (bit-identical to the rows of the functions above).
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library, and
  * only as the checker or the timed CPU baseline -- never as a path of the shipped operator.

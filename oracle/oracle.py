@@ -44,6 +44,10 @@ def lib():
             f.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, real, c_int, vp, vp, vp,
                           c_int]
             f.restype = c_int
+            f = getattr(L, f"oracle_rows_{suffix}")
+            f.argtypes = [vp, vp, vp, vp, i64, i64, real, c_int, vp, i64, vp, i64, vp, vp, vp,
+                          vp, vp, c_int]
+            f.restype = c_int
         L.oracle_gather_f32.argtypes = [vp, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp]
         L.oracle_gather_f32.restype = c_int
         _lib = L
@@ -95,6 +99,29 @@ def backward(q, k, v, o, l_, d_o, scale: float, causal: bool, dtype=np.float32,
     if rc != 0:
         raise RuntimeError(f"oracle backward failed ({rc})")
     return dq, dk, dv
+
+
+def rows(q, k, v, d_o, scale: float, causal: bool, query_rows, key_rows, dtype=np.float64,
+         threads: int | None = None):
+    """One [s, d] slice at sampled rows, without [s, s] buffers (long sequences): (O, L, dQ)
+    at `query_rows` and (dK, dV) at `key_rows`, equal bit for bit to the rows of forward /
+    backward in the same precision (src/lib.rs:241-299)."""
+    q, k, v, d_o = (_prep(x, dtype) for x in (q, k, v, d_o))
+    s, d = q.shape
+    ri = np.ascontiguousarray(query_rows, dtype=np.int64)
+    ki = np.ascontiguousarray(key_rows, dtype=np.int64)
+    o = np.empty((len(ri), d), dtype)
+    l_ = np.empty(len(ri), dtype)
+    dq = np.empty((len(ri), d), dtype)
+    dk, dv = np.empty((len(ki), d), dtype), np.empty((len(ki), d), dtype)
+    suffix = "f32" if dtype == np.float32 else "f64"
+    rc = getattr(lib(), f"oracle_rows_{suffix}")(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(d_o), s, d, scale, int(causal), _ptr(ri), len(ri),
+        _ptr(ki), len(ki), _ptr(o), _ptr(l_), _ptr(dq), _ptr(dk), _ptr(dv),
+        threads or default_threads())
+    if rc != 0:
+        raise RuntimeError(f"oracle rows failed ({rc})")
+    return o, l_, dq, dk, dv
 
 
 def gather(storage, start: int, dims, strides):

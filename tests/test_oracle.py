@@ -177,6 +177,26 @@ def test_fp32_vs_fp64_seeded(orc):
             assert orc.rel_fro(a, r) < 2e-6
 
 
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("s,causal", [(1, False), (97, False), (97, True), (200, True)])
+def test_rows_equal_full_slices(orc, s, causal, dtype):
+    """oracle_rows_f64 / _f32 (sampled rows without [s, s] buffers, for long sequences) give
+    the full forward / backward's rows of the same precision bit for bit: O, L and dQ at query
+    rows, dK and dV at key rows (first, last and random rows)."""
+    rng = np.random.default_rng(s + causal)
+    q, k, v, g = (rng.standard_normal((1, 1, s, 64)).astype(dtype) for _ in range(4))
+    o, l_ = orc.forward(q, k, v, 0.125, causal, dtype=dtype)
+    dq, dk, dv = orc.backward(q, k, v, o, l_, g, 0.125, causal, dtype=dtype)
+    qi = np.unique(np.r_[0, s - 1, rng.integers(0, s, 7)])
+    ki = np.unique(np.r_[0, s - 1, rng.integers(0, s, 5)])
+    got = orc.rows(q[0, 0], k[0, 0], v[0, 0], g[0, 0], 0.125, causal, qi, ki, dtype=dtype)
+    want = (o[0, 0][qi], l_[0, 0][qi], dq[0, 0][qi], dk[0, 0][ki], dv[0, 0][ki])
+    for name, a, b in zip(("o", "l", "dq", "dk", "dv"), got, want):
+        assert np.array_equal(a, b), name
+    with pytest.raises(RuntimeError):
+        orc.rows(q[0, 0], k[0, 0], v[0, 0], g[0, 0], 0.125, causal, [s], ki)
+
+
 def test_gather_matches_strides(orc):
     rng = np.random.default_rng(6)
     storage = rng.standard_normal(4000).astype(np.float32)

@@ -1102,6 +1102,48 @@ def test_random_qkv_cases(orc, cuda, seed):
     check_against_oracle(orc, got, vals, scale, causal)
 
 
+# --- a very long sequence: the turn hand-over past the workspace cap ------------------------
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_very_long_sequence(orc, cuda, causal):
+    """One head of s 32816 (not a multiple of 64) through fused_attention_qkv: the split dQ sum
+    would need more than the 4 GiB workspace cap and one (b, h) pair cannot be chunked, so the
+    backward takes the turn hand-over. O, L and dQ at 48 query rows and dK, dV at 48 key rows
+    (the first, the last, random ones) against the oracle's rows (oracle.rows: the composed
+    formulas of src/lib.rs:241-299 without [s, s] buffers, bit-identical to the slice-wise
+    oracle), at the bar of the other parity tests: within 2e-6 normwise of fp64, or 1.5x the fp32
+    composed path's own error on the same rows. Both fp32 paths sum over s terms, so at this
+    length that floor is what binds."""
+    s, d = 32816, 64
+    L = _lib.lib()
+    assert L.fattn_bwd_workspace_split_bytes(1, 1, s, d) > 4 << 30
+    assert L.fattn_bwd_workspace_bytes(1, 1, s, d) == L.fattn_bwd_workspace_min_bytes(1, 1, s, d)
+    rng = np.random.default_rng(32816 + causal)
+    x = rng.standard_normal((1, s, 3 * d)).astype(np.float32)
+    w = rng.standard_normal((1, s, d)).astype(np.float32)
+    say(f"s {s} causal={causal}: turn hand-over")
+    qkv = torch.from_numpy(x).to(cuda)
+    out, grad = run("fused_qkv", qkv, torch.from_numpy(w).to(cuda), 1, d, causal, 0.125)
+    _, lse = forward_qkv_c(qkv, 1, 0.125, causal)
+    _, grad2 = run("fused_qkv", qkv, torch.from_numpy(w).to(cuda), 1, d, causal, 0.125)
+    assert torch.equal(bits(grad), bits(grad2)), "backward reruns differ"
+    rows = np.unique(np.r_[0, s - 1, rng.integers(0, s, 46)])
+    keys = np.unique(np.r_[0, s - 1, rng.integers(0, s, 46)])
+    q, k, v = (x[0, :, i * d:(i + 1) * d] for i in range(3))
+    ref = orc.rows(q, k, v, w[0], 0.125, causal, rows, keys, dtype=np.float64)
+    f32 = orc.rows(q, k, v, w[0], 0.125, causal, rows, keys, dtype=np.float32)
+    o, g = out.cpu().numpy()[0], grad.cpu().numpy()[0]
+    got = (o[rows], lse.cpu().numpy()[0, 0, rows], g[rows, :d], g[keys, d:2 * d], g[keys, 2 * d:])
+    check_lse(got[1], ref[1], f32[1], f"s{s}")
+    for name, a, r, fl in zip(("o", "dq", "dk", "dv"), got[:1] + got[2:], ref[:1] + ref[2:],
+                              f32[:1] + f32[2:]):
+        assert np.all(np.isfinite(a)), name
+        err, floor = orc.rel_fro(a, r), orc.rel_fro(fl, r)
+        bar = max(REL_TOL, 1.5 * floor)
+        say(f"  {name}: {err:.2e} (fp32 composed {floor:.2e}, bar {bar:.2e})")
+        assert err <= bar, f"{name}: normwise error {err:.3e} > {bar:.3e}"
+
+
 # --- the split dQ sum by chunks of (b, h) (a workspace that holds some pairs' partials) ---------
 
 @pytest.mark.parametrize("causal", [False, True])
