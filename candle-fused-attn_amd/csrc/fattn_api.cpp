@@ -305,7 +305,8 @@ int check_bwd_main(const char* who, View q, View k, View v, const float* o, View
 
 int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d_o,
                  const float* lse, float* dqkv, void* ws, size_t ws_bytes, int64_t b, int64_t h,
-                 int64_t s, int64_t d, float scale, int causal, void* stream) {
+                 int64_t s, int64_t d, float scale, int causal, void* stream,
+                 bool sums_final = false) {
   if (int rc = check_bwd_main(who, q, k, v, o, d_o, lse, dqkv, b, h, s, d)) return rc;
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
@@ -313,9 +314,19 @@ int run_bwd_main(const char* who, View q, View k, View v, const float* o, View d
                                          p.done, p.epoch, next_epoch(), p.turn, p.ctrl,
                                          static_cast<int>(b), static_cast<int>(h),
                                          static_cast<int>(s), static_cast<int>(d), scale,
-                                         causal ? 1 : 0, 0, static_cast<int>(b * h), stream);
+                                         causal ? 1 : 0, 0, static_cast<int>(b * h),
+                                         sums_final ? 1 : 0, stream);
   if (err) return hip_fail(err, "backward step 2 launch");
   return ok();
+}
+
+// Whether `stream` is capturing a HIP graph (or that cannot be told): then step 3 runs after
+// step 2 even where step 2 sums every tile, because it also clears the sums' flags, which a
+// replay of the graph (the same epoch) needs.
+bool capturing(void* stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &st) != hipSuccess) return true;
+  return st != hipStreamCaptureStatusNone;
 }
 
 // Step 3: in split mode (the workspace holds the partials) dQ from the partials; else nothing.
@@ -348,14 +359,18 @@ int run_backward_chunked(const char* who, View q, View k, View v, const float* o
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, 1, chunk, s, d, &p)) return rc;
   if (!p.part) return fail(FATTN_EWORKSPACE, std::string(who) + ": workspace too small");
+  const bool eager = !capturing(stream);
   for (int64_t bh0 = 0; bh0 < b * h; bh0 += chunk) {
     const int n = static_cast<int>(std::min(chunk, b * h - bh0));
+    const bool final_sums =
+        eager && fattn::bwd_step2_sums_all(n, b, h, s, static_cast<int>(d), causal ? 1 : 0);
     int err = fattn::launch_bwd_main(q, k, v, d_o, o, lse, p.dsum, dqkv, p.part, p.arrive, p.done,
                                      p.epoch, next_epoch(), p.turn, p.ctrl, static_cast<int>(b),
                                      static_cast<int>(h), static_cast<int>(s),
                                      static_cast<int>(d), scale, causal ? 1 : 0,
-                                     static_cast<int>(bh0), n, stream);
+                                     static_cast<int>(bh0), n, final_sums ? 1 : 0, stream);
     if (err) return hip_fail(err, "backward step 2 launch");
+    if (final_sums) continue;
     err = fattn::launch_bwd_dq(p.part, p.done, p.arrive, p.epoch, dqkv, static_cast<int>(b),
                                static_cast<int>(h), static_cast<int>(s), static_cast<int>(d),
                                scale, causal ? 1 : 0, static_cast<int>(bh0), n, stream);
@@ -384,10 +399,16 @@ int run_backward(const char* who, View q, View k, View v, const float* o, View d
                                 causal, chunk, stream);
   }
   if (int rc = run_bwd_prep(who, o, d_o, ws, ws_bytes, b, h, s, d, stream)) return rc;
+  // Step 3 only where step 2's sums may leave tiles (or a graph is being captured).
+  const bool final_sums = ws && ws_bytes >= fattn::workspace_layout(b, h, s, d).bytes_split &&
+                          fattn::bwd_step2_sums_all(b * h, b, h, s, static_cast<int>(d),
+                                                    causal ? 1 : 0) &&
+                          !capturing(stream);
   if (int rc = run_bwd_main(who, q, k, v, o, d_o, lse, dqkv, ws, ws_bytes, b, h, s, d, scale,
-                            causal, stream)) {
+                            causal, stream, final_sums)) {
     return rc;
   }
+  if (final_sums) return ok();
   return run_bwd_dq(who, dqkv, ws, ws_bytes, b, h, s, d, scale, causal, stream);
 }
 
@@ -734,9 +755,10 @@ int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
 // kernel runs (fattn_internal.h). A summing unit is a workgroup appended to step 2's grid
 // (non-causal) or a key block's own workgroup summing its diagonal tiles (causal). out[0]:
 // workgroups appended to step 2's grid; out[1]: summing units with tiles to sum; out[2]:
-// violations -- a unit waits for a key block that runs on another XCD or later in the grid, a
-// causal unit sums a tile it is not the last contributor of, xcd_remap and item_xcd disagree, or
-// a workgroup past the plan's range has a target; out[3]: query tiles two units would both sum;
+// violations -- a unit waits for a key block later in the grid, a non-causal unit for one that
+// xcd_remap puts on another XCD (the plan's dispatch order), a causal unit sums a tile it is not
+// the last contributor of, xcd_remap and item_xcd disagree, or a workgroup past the plan's range
+// has a target; out[3]: query tiles two units would both sum;
 // out[4]: query tiles summed; out[5]: keys per key block (bwd_split_keys).
 int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int causal,
                              int64_t out[6]) {
@@ -784,8 +806,7 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
         const int id = kb * BH + bh, need = need_of(j1);
         if (need != kb + 1 || need_of(j0 + 1) != kb + 1) ++bad;  // not its last contributor
         for (int k = 0; k < need; ++k) {
-          const int idk = k * BH + bh;
-          if (idk > id || (idk & 7) != (id & 7)) ++bad;
+          if (k * BH + bh > id) ++bad;  // a contributor later in the grid
         }
         mark(bh, j0, j1);
       }
@@ -821,6 +842,12 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
 // Test hook (not declared in include/fattn.h): step 2's dQ sums on (1, the default) or off (0:
 // step 3 sums every tile) for every later backward of the process. Returns the previous setting.
 int fattn_internal_step2_sums(int on) { return fattn::set_step2_sums(on != 0) ? 1 : 0; }
+
+// Test hook (not declared in include/fattn.h): step 2's non-causal summing workgroups of XCD x
+// sum the (b, h)s whose key blocks ran on XCD x + shift (mod 8) in every later backward of the
+// process (0, the default: their own XCD's), so that a test can make every sum read partials
+// written on another XCD. Returns the previous shift.
+int fattn_internal_sum_shift(int shift) { return fattn::set_sum_shift(shift); }
 
 int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                      int64_t s, void* stream, int* status) {

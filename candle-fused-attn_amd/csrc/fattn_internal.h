@@ -81,10 +81,12 @@ __host__ __device__ inline int item_xcd(int item, int total) {
   return item >= full ? (item & 7) : item / (full >> 3);
 }
 
-// The dQ sums in step 2. `per` (b, h)s per XCD have every key block on that XCD: non-causal, the
-// (b, h)-major key blocks under xcd_remap, when F is a whole number of (b, h)s; causal, key block
-// kb of (b, h) is workgroup kb b h + bh, on XCD bh mod 8, when 8 divides b h. per = 0: no sums
-// (step 3 sums every tile). nchunk = chunks of kSumTiles query tiles per (b, h) (non-causal).
+// The dQ sums in step 2. Non-causal: `per` (b, h)s per XCD have every key block on that XCD (the
+// (b, h)-major key blocks under xcd_remap, when F is a whole number of (b, h)s), and the
+// workgroups appended for XCD x sum those, in the order their key blocks were dispatched (the
+// partials are read at device scope, so the XCD is not needed for correctness, only for that
+// order); causal: per = 1, every key block sums the tiles it completes. per = 0: no sums (step 3
+// sums every tile). nchunk = chunks of kSumTiles query tiles per (b, h) (non-causal).
 struct SumPlan {
   int per, nchunk;
 };
@@ -93,7 +95,7 @@ __host__ __device__ inline SumPlan sum_plan(int BH, int nkb, int ntile, int d, i
   // (At d 128 the split kernel has the non-causal tail sums only.)
   if ((d > 64 && causal) || nkb > kSumMaxBlocks || BH <= 0) return p;
   if (causal) {
-    p.per = BH % 8 == 0 ? BH / 8 : 0;
+    p.per = 1;  // (a flag: every key block sums the tiles it completes)
   } else {
     const int f = ((nkb * BH) & ~7) >> 3;
     p.per = f > 0 && f % nkb == 0 ? f / nkb : 0;
@@ -121,6 +123,10 @@ int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal);
 // Step 2's sums on (the default) or off for every later backward of the process, so that a test
 // can compare both; returns the previous setting.
 bool set_step2_sums(bool on);
+// Test hook: the non-causal summing workgroups of XCD x sum the (b, h)s of XCD x + shift (mod 8)
+// in every later launch, so that their partials come from another XCD; returns the previous
+// shift.
+int set_sum_shift(int shift);
 // Step 3's grid: one workgroup per query tile, or (with step 2's sums) at most 256 workgroups
 // that each check a range of tiles and sum those not done.
 int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal);
@@ -141,7 +147,10 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
                     const float* dsum, float* dqkv, float* part, unsigned long long* arrive,
                     unsigned long long* done, unsigned long long* epoch_slot,
                     unsigned long long epoch, int* turn, int* ctrl, int b, int h, int s, int d,
-                    float scale, int causal, int bh0, int nbh, void* stream);
+                    float scale, int causal, int bh0, int nbh, int sums_final, void* stream);
+// Whether step 2's sums cover every query tile of a launch over nbh of the b h pairs (then no
+// step 3 need follow it).
+bool bwd_step2_sums_all(int64_t nbh, int64_t b, int64_t h, int64_t s, int d, int causal);
 // Step 3: dQ of every query tile that step 2 did not sum (done: null, none did); then the done
 // flags and arrival slots are zeroed. bh0, nbh: as step 2's.
 int launch_bwd_dq(const float* part, unsigned long long* done, unsigned long long* arrive,

@@ -86,6 +86,22 @@ __device__ __forceinline__ void st4_nt(float* p, f4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
 }
 __device__ __forceinline__ f4 zero4() { return f4{0.0f, 0.0f, 0.0f, 0.0f}; }
+// 16 bytes stored / loaded at device scope (cache-policy bit sc1: through to the coherence point
+// that all XCDs share), as buffer accesses from a wave-uniform base that cover `bytes` bytes
+// (accesses past them are dropped / read 0). The dQ partials and their sums in step 2 use them,
+// so that a sum may read partials written by a key block on another XCD.
+constexpr int kScDevice = 16;              // the buffer access's cache-policy operand: sc1
+constexpr int kRsrcWord3 = 0x00020000;     // gfx9 buffer descriptor: 32-bit data format
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, bytes, kRsrcWord3);
+}
+__device__ __forceinline__ void st4_dev(__amdgpu_buffer_rsrc_t r, unsigned off, f4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, off, 0, kScDevice);
+}
+__device__ __forceinline__ f4 ld4_dev(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kScDevice));
+}
 
 // A lane of x through a DPP lane permutation (VALU, no LDS round trip).
 template <int CTRL>
@@ -747,6 +763,12 @@ struct BwdArgs {
   // chunks, each with its partials, arrival slots and done flags at the start of the workspace;
   // the turn path always covers all, bh0 0 and nbh b h).
   int bh0, nbh;
+  // 1: no step 3 follows (step 2's sums cover every tile): a sum's wait is bounded only by
+  // kSumPollsFinal and one that gives up raises the guard word and leaves NaN in its rows.
+  int sums_final;
+  // Test hook (0 in use): the non-causal summing workgroups of XCD x take the (b, h)s of XCD
+  // x + sum_shift, so that every sum reads partials written on another XCD.
+  int sum_shift;
 };
 
 // Staggered walks make a key block wait on blocks of its own (b, h) that hold later tickets; that
@@ -1046,12 +1068,14 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   constexpr int kPartStores = kNS * kDQ;
   auto store_part = [&](int q0p, const f4 (&part)[kDQ][kNS]) {
     if (!wave_dq) return;
-    float* dst = a.part + ((static_cast<int64_t>(kb) * BH + bh) * a.ntile + q0p / kQT) *
-                              (kQT * D) + 4 * lane;
+    const float* dst = a.part + ((static_cast<int64_t>(kb) * BH + bh) * a.ntile + q0p / kQT) *
+                                    (kQT * D);
 #pragma unroll
     for (int j = 0; j < kDQ; ++j) {
 #pragma unroll
-      for (int m = 0; m < kNS; ++m) st4(dst + (m * kDT + w + 4 * j) * 256, part[j][m]);
+      for (int m = 0; m < kNS; ++m) {
+        st4_dev(dev_rsrc(dst + (m * kDT + w + 4 * j) * 256, 1024), 16u * lane, part[j][m]);
+      }
     }
   };
   // After stage 2's stores completed (vmcnt(0) and a barrier): the next contributor's turn.
@@ -1295,32 +1319,38 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // dQ sums inside step 2 (split, D <= 64). Step 3 moves 118 MB at config 2 after step 2's tail,
 // where the CUs run fewer and fewer key blocks; step 2 does those sums itself instead.
 // bwd_sum_range sums query tiles j0 .. j1 - 1 of one (b, h) once every key block they need has
-// finished. Each key block, once its partials are stored, writes the launch's epoch or'ed with its
-// XCD to its arrival slot (agent scope: written through to the coherence point, as the turn
-// hand-over's counters). Wave 0 polls the (b, h)'s slots (agent-scope loads) until every one it
-// needs holds this launch's epoch, sleeping between polls, giving up after kSumPolls. The tiles are
-// summed only if every key block ran on this workgroup's XCD: all partials are then in this XCD's
-// L2 (or written back from it). The sum is step 3's, operation for operation: float4 i of a tile's
-// partials in key-block order, times scale (so the results are bit-identical whichever kernel sums
-// a tile), stored from fragment order straight into dQ rows (16 lanes write 64 contiguous bytes).
-// Then the tiles' done flags (the epoch); step 3 sums the tiles without one, so a key block on
-// another XCD, or a poll that gave up, only leaves work to step 3.
+// finished. The partials are stored and loaded at device scope (st4_dev / ld4_dev: through to the
+// coherence point that the XCDs share, whose L2s are not coherent with each other), so a sum may
+// read partials that a key block on any XCD wrote. Each key block, once its partial stores have
+// completed, writes the launch's epoch or'ed with its XCD to its arrival slot (a device-scope
+// store, as the turn hand-over's counters). Wave 0 polls the (b, h)'s slots (device-scope loads)
+// until every one it needs holds this launch's epoch, sleeping between polls. The sum is step 3's,
+// operation for operation: float4 i of a tile's partials in key-block order, times scale (so the
+// results are bit-identical whichever kernel sums a tile), stored from fragment order straight
+// into dQ rows (16 lanes write 64 contiguous bytes). Then the tiles' done flags (the epoch), which
+// step 3 checks when it runs: after a kernel-level step 2, while a graph is captured (step 3 also
+// clears the flags a replay, with the same epoch, must not see), or where the plan leaves tiles.
+// Otherwise no step 3 follows (sums_final): a wait then gives up only after kSumPollsFinal polls
+// (about half a second), raising the guard word and writing NaN into the tiles' rows; with step 3
+// to follow it gives up after kSumPolls and leaves the tiles to step 3.
 // Who sums:
 //   non-causal: workgroups appended to step 2's grid (in-order dispatch starts them only once every
 //   key block has been dispatched). Workgroup n_main + 8 m + x (on XCD x: workgroups go to the
-//   XCDs round robin on MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks all
-//   run on XCD x (sum_target: plan.per (b, h)s per XCD, kSumTiles tiles per chunk, in the order
-//   their key blocks were dispatched; the host sizes the grid from the same plan);
+//   XCDs round robin on MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks
+//   xcd_remap put on XCD x (sum_target: plan.per (b, h)s per XCD, kSumTiles tiles per chunk, in the
+//   order their key blocks were dispatched, so the earliest sums wait for the earliest key blocks;
+//   the host sizes the grid from the same plan);
 //   causal: key block kb's own workgroup, after its walk, sums the tiles whose last contributor it
-//   is (own_tiles: its diagonal tiles 4 kb .. 4 kb + 3), which need key blocks 0 .. kb. Their
-//   workgroups kb' b h + bh come earlier in the grid and run on the same XCD (8 divides b h). No
-//   workgroup is appended: a tile is summed as soon as its last key block finishes, while other
-//   key blocks still run, where summing workgroups would start only after the last key block.
-//   At config 4 that is step 2 1202 -> 1116 us, at config 3 97.1 -> 93.6 us.
-// Every poll ends: the key blocks waited for have smaller workgroup numbers on the same XCD, so
-// they were dispatched before the polling workgroup and run to completion whatever it does.
+//   is (own_tiles: its diagonal tiles 4 kb .. 4 kb + 3), which need key blocks 0 .. kb, whose
+//   workgroups kb' b h + bh come earlier in the grid. No workgroup is appended: a tile is summed as
+//   soon as its last key block finishes, while other key blocks still run, where summing
+//   workgroups would start only after the last key block. At config 4 that is step 2 1202 -> 1116
+//   us, at config 3 97.1 -> 93.6 us.
+// Every poll ends: the key blocks waited for have smaller workgroup numbers, so they were
+// dispatched before the polling workgroup and run to completion whatever it does.
 // kSumTiles query tiles per summing workgroup: at config 2, 1, 2 or 15 were slower and 4 the same.
 constexpr int kSumPolls = 4096;
+constexpr int kSumPollsFinal = 1 << 20;
 template <int D, int NT>
 __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, int j1,
                                               unsigned* flag) {
@@ -1330,30 +1360,41 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
   // query.
   const int need = a.causal ? min(nkb - 1, min(a.S - 1, j1 * kQT - 1) / a.kkeys) + 1 : nkb;
   if (tid < 64) {
-    unsigned xcc;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-    const unsigned long long mine = a.epoch | (xcc & 7u);
     const unsigned long long* slots = a.arrive + static_cast<int64_t>(bh) * nkb;
-    bool all_mine = false;
-    for (int it = 0; it < kSumPolls; ++it) {
-      bool arrived = true, here = true;
+    const int polls = a.sums_final ? kSumPollsFinal : kSumPolls;
+    bool all = false;
+    for (int it = 0; it < polls; ++it) {
+      bool arrived = true;
       for (int kb = tid; kb < need; kb += 64) {
         const unsigned long long v =
             __hip_atomic_load(slots + kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         arrived = arrived && (v & ~7ull) == a.epoch;
-        here = here && v == mine;
       }
       if (__builtin_amdgcn_ballot_w64(!arrived) == 0) {
-        all_mine = __builtin_amdgcn_ballot_w64(!here) == 0;
+        all = true;
         break;
       }
       __builtin_amdgcn_s_sleep(16);  // about 1000 cycles between polls
     }
-    if (tid == 0) *flag = all_mine ? 1u : 0u;
+    if (tid == 0) *flag = all ? 1u : 0u;
+    if (tid == 0 && !all && a.sums_final) {
+      __hip_atomic_store(a.ctrl + kCtrlGuard, 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
-  if (*flag == 0u) return;
   const int b = (a.bh0 + bh) / a.H, h = (a.bh0 + bh) % a.H, S = a.S;
+  const int64_t row_stride0 = static_cast<int64_t>(3) * a.H * D;
+  if (*flag == 0u) {
+    if (a.sums_final) {
+      // No step 3 follows: the tiles' dQ rows get NaN (the failure shows in the output).
+      float* dq0 = a.dqkv + static_cast<int64_t>(b) * S * row_stride0 + static_cast<int64_t>(h) * D;
+      for (int e = tid; e < (j1 - j0) * kQT * D; e += kThreads) {
+        const int q = j0 * kQT + e / D;
+        if (q < S) dq0[q * row_stride0 + e % D] = __builtin_nanf("");
+      }
+    }
+    return;
+  }
   const int64_t slot = static_cast<int64_t>(BH) * ntile * (kQT * D);
   const int64_t row_stride = static_cast<int64_t>(3) * a.H * D;
   float* const dq_bh =
@@ -1371,7 +1412,7 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
       cnt[jj] = j0 + jj >= j1 ? 0
                 : a.causal ? min(nkb - 1, min(S - 1, j * kQT + kQT - 1) / a.kkeys) + 1
                            : nkb;
-      src[jj] = a.part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D) + 4 * i;
+      src[jj] = a.part + (static_cast<int64_t>(bh) * ntile + j) * (kQT * D);
     }
     for (int kb0 = 0; kb0 < need; kb0 += 4) {
       f4 x[NT][4];
@@ -1380,7 +1421,10 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int kb = kb0 + k;
-          x[jj][k] = kb < cnt[jj] ? ld4(src[jj] + min(kb, cnt[jj] - 1) * slot) : zero4();
+          x[jj][k] = kb < cnt[jj]
+                         ? ld4_dev(dev_rsrc(src[jj] + min(kb, cnt[jj] - 1) * slot, kQT * D * 4),
+                                   16u * static_cast<unsigned>(i))
+                         : zero4();
         }
       }
 #pragma unroll
@@ -1413,7 +1457,7 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
 template <int D>
 __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, unsigned* flag) {
   int bh, j0;
-  if (!sum_target(a.plan, x, m, a.nbh, a.causal, &bh, &j0)) return;
+  if (!sum_target(a.plan, (x + a.sum_shift) & 7, m, a.nbh, a.causal, &bh, &j0)) return;
   bwd_sum_range<D, kSumTiles>(a, bh, j0, min(a.ntile, j0 + kSumTiles), flag);
 }
 
@@ -1461,8 +1505,11 @@ bwd_split_kernel(BwdArgs a) {
   constexpr int kDqGroups = 4 / kDT;
   const int dt = w % kDT;
   auto dq_on = [&](int jt) { return kDqGroups == 1 || w / kDT == (jt + id) % kDqGroups; };
-  // No turn waits here: the guard word reads 0.
-  if (id == 0 && tid == 0) a.ctrl[kCtrlGuard] = 0;
+  // No turn waits here: the guard word reads 0 (unless a final sum's wait gave up; written
+  // through, as that raise is, so that no copy of it lingers in this XCD's L2).
+  if (id == 0 && tid == 0) {
+    __hip_atomic_store(a.ctrl + kCtrlGuard, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // The key block: non-causal, (b, h)-major with the key blocks of one (b, h) on one XCD (they
   // read the same Q and dO tiles at about the same time); causal, key-block-major round-robin over
@@ -1554,8 +1601,8 @@ bwd_split_kernel(BwdArgs a) {
   // The dQ partial of query tile j: the wave's 16 x 16 fragment (dim tile dt) in the key block's
   // slot, fragment order (register r of lane (lo, g) at 4 lane + r: query 16 j + 4 g + r, dim
   // 16 dt + lo); step 3 (dq_kernel) sums the slots.
-  float* const slot = a.part + (static_cast<int64_t>(kb) * BH + bh) * a.ntile * (kQT * D) +
-                      256 * dt + 4 * lane;
+  const float* const slot =
+      a.part + (static_cast<int64_t>(kb) * BH + bh) * a.ntile * (kQT * D) + 256 * dt;
 
   f4 dva[KG][kDT], dka[KG][kDT];
 #pragma unroll
@@ -1567,7 +1614,9 @@ bwd_split_kernel(BwdArgs a) {
     }
   }
   f4 p1 = zero4();  // the dQ fragment of the last tile (stored at the start of the next)
-  auto store_frag = [&](int j) { st4(slot + j * (kQT * D), p1); };
+  auto store_frag = [&](int j) {
+    st4_dev(dev_rsrc(slot + j * (kQT * D), 1024), 16u * static_cast<unsigned>(lane), p1);
+  };
 
   gload(0, Const<0>{});
   if (nsteps > 1) gload(1, Const<1>{});
@@ -1924,8 +1973,10 @@ int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQ
 bool bwd_needs_prep(bool split, int d) { return !split || d > 64; }
 namespace {
 std::atomic<int> g_step2_sums{1};
+std::atomic<int> g_sum_shift{0};
 }  // namespace
 bool set_step2_sums(bool on) { return g_step2_sums.exchange(on ? 1 : 0) != 0; }
+int set_sum_shift(int shift) { return g_sum_shift.exchange(shift & 7); }
 
 int bwd_split_keys(int64_t b, int64_t h, int64_t s, int d, int causal) {
   // 128-key blocks (two 16-key groups per wave, 2 waves per SIMD): half the dQ partials and half
@@ -1960,6 +2011,14 @@ int64_t dq_grid_of(int64_t nbh, int64_t s, int d, int causal, int keys) {
   return std::min(tiles, g);
 }
 }  // namespace
+bool bwd_step2_sums_all(int64_t nbh, int64_t b, int64_t h, int64_t s, int d, int causal) {
+  const int keys = d <= 64 ? bwd_split_keys(b, h, s, d, causal) : kBwdKeys;
+  if (!step2_sums_of(nbh, s, d, causal, keys)) return false;
+  const int nkb = static_cast<int>((s + keys - 1) / keys);
+  const int ntile = static_cast<int>((s + kQT - 1) / kQT);
+  const SumPlan p = sum_plan(static_cast<int>(nbh), nkb, ntile, d, causal);
+  return causal ? p.per > 0 : int64_t{8} * p.per == nbh;
+}
 bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal) {
   return step2_sums_of(b * h, s, d, causal, bwd_split_keys(b, h, s, d, causal));
 }
@@ -1997,7 +2056,8 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
                     const float* dsum, float* dqkv, float* part, unsigned long long* arrive,
                     unsigned long long* done, unsigned long long* epoch_slot,
                     unsigned long long epoch, int* turn, int* ctrl, int b, int h, int s, int d,
-                    float scale, int causal, int bh0, int nbh, void* stream) {
+                    float scale, int causal, int bh0, int nbh, int sums_final,
+                    void* stream) {
   int nkb = (s + kBwdKeys - 1) / kBwdKeys, ntile = (s + kQT - 1) / kQT;
   const bool split = part != nullptr;
   // The split path's grid is that of the chunk (nbh pairs) with the whole's key blocks; the
@@ -2015,7 +2075,8 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   const SumPlan plan = sum_plan(nbh, nkb, ntile, d, causal);
   BwdArgs a{q,    k,     v,    d_o,  o,    lse,   dsum,       dqkv,  part,
             arrive, done, epoch_slot, epoch, static_cast<int>(nmain), plan, turn, ctrl, b, h, s,
-            nkb,  ntile, scale, causal, stagger, kkeys, bh0, nbh};
+            nkb,  ntile, scale, causal, stagger, kkeys, bh0, nbh,
+            arrive != nullptr && sums_final ? 1 : 0, g_sum_shift.load(std::memory_order_relaxed)};
   void* args[] = {&a};
   if (split && d <= 64) {
     const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32, 1>)

@@ -223,8 +223,10 @@ const char* fattn_last_error(void);
 const char* fattn_version(void);
 
 /* Synchronises `stream`, then reads the backward's guard word from `workspace` into *status:
- * 0 = every dQ turn wait ended normally; nonzero = some wait hit its spin bound (the turn
- * protocol failed, results are invalid). For tests and debugging; any head_dim. */
+ * 0 = every dQ wait ended normally; nonzero = results are invalid: 1, a turn wait of the turn
+ * hand-over hit its spin bound; 2, a ticket out of range (step 1 did not run on this
+ * workspace); 3, a dQ sum of step 2 with no step 3 after it gave up waiting (the dQ rows
+ * concerned hold NaN). For tests and debugging; any head_dim. */
 int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                      int64_t s, void* stream, int* status);
 

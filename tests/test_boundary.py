@@ -321,15 +321,16 @@ def expected_keys(bh, s, d, causal):
 
 
 def expected_sum_bh(bh, s, causal, keys=64):
-    """Restated from the schedule's definition: the (b, h)s whose key blocks all run on one XCD
-    when workgroups go to the 8 XCDs round-robin. Non-causal: (b, h)-major key blocks under
-    xcd_remap, XCD x holding items [x F, (x + 1) F), F = floor(nkb b h / 8) -- a whole number of
-    (b, h)s per XCD or no sums; causal: 8 must divide b h."""
+    """Restated from the schedule's definition. Non-causal: the (b, h)s whose key blocks all run
+    on one XCD when workgroups go to the 8 XCDs round-robin -- (b, h)-major key blocks under
+    xcd_remap, XCD x holding items [x F, (x + 1) F), F = floor(nkb b h / 8): a whole number of
+    (b, h)s per XCD or no sums; causal: every (b, h) (the partials are read at device scope, so a
+    key block sums its tiles whatever XCDs its contributors ran on)."""
     nkb = -(-s // keys)
     if nkb > 256:
         return 0
     if causal:
-        return bh if bh % 8 == 0 else 0
+        return bh
     f = (nkb * bh) // 8
     return 8 * (f // nkb) if f > 0 and f % nkb == 0 else 0
 
@@ -337,10 +338,10 @@ def expected_sum_bh(bh, s, causal, keys=64):
 @pytest.mark.parametrize("causal", [False, True])
 def test_step2_dq_sum_schedule(causal):
     """Step 2's dQ sums, over many shapes (the kernel's own scheduling functions, run on the
-    host): every key block a summing unit waits for runs on that unit's XCD and earlier in the
-    grid, no target lies past b h (the case a rounded-up per-XCD count once produced: nkb = 1, b h
+    host): every key block a summing unit waits for comes earlier in the grid (and, non-causal,
+    runs on that unit's XCD: the plan's order), no target lies past b h (the case a rounded-up per-XCD count once produced: nkb = 1, b h
     not a multiple of 8, e.g. h 17 s 50), no tile is summed twice, and exactly the (b, h)s the
-    schedule's definition puts wholly on one XCD are summed, every one of their tiles.
+    schedule's definition sums are summed, every one of their tiles.
     Non-causal, the units are workgroups appended to the grid, ceil(ntile / 3) per (b, h) (every
     head_dim); causal, every key block's own workgroup sums its diagonal tiles (none appended; d 64
     and below: step 3 sums them at d 128)."""

@@ -470,8 +470,8 @@ def test_config1_general_path(orc, cuda):
     assert torch.equal(bits(o_op.transpose(1, 2)), bits(o.detach()))
 
 
-def seeded_qkv(orc, b, h, s, seed, cuda):
-    x, dout = orc.seeded_qkv_inputs(b, h, s, seed)
+def seeded_qkv(orc, b, h, s, seed, cuda, d=64):
+    x, dout = orc.seeded_qkv_inputs(b, h, s, seed, d=d)
     return x, dout, torch.from_numpy(x).to(cuda), torch.from_numpy(dout).to(cuda)
 
 
@@ -801,38 +801,118 @@ def step2_summed_tiles(qkv, dout, h, d, causal, grad_want):
     return done == epoch
 
 
-@pytest.mark.parametrize("causal", [False, True])
-def test_step2_sums_equal_step3_sums_at_scale(orc, cuda, causal):
-    """Step 2's tail sums read the partials of key blocks that ran on their own XCD, from that
-    XCD's L2, with plain loads after an agent-scope arrival flag; step 3 reads them after a kernel
-    boundary. At config 2's shape (384 heads, every tile summed in step 2), the backward with step
-    2's sums switched off (step 3 sums every tile) must give the same bits, on three runs."""
-    L = _lib.lib()
-    f = L.fattn_internal_step2_sums
+def _hook(name):
+    f = getattr(_lib.lib(), name)
     f.argtypes = [ctypes.c_int]
     f.restype = ctypes.c_int
+    return f
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_step2_sums_equal_step3_sums_at_scale(orc, cuda, causal):
+    """Step 2's sums read the dQ partials at device scope after a device-scope arrival flag, in
+    the same kernel; step 3 reads them after a kernel boundary. At config 2's shape (384 heads,
+    every tile summed in step 2, so that no step 3 follows an eager backward), the backward with
+    step 2's sums switched off (step 3 sums every tile) must give the same bits, on three runs;
+    non-causal also with the summing workgroups of XCD x given the heads of XCD x + 3 (a test
+    hook), so that every sum reads partials written on another XCD."""
+    sums, shift = _hook("fattn_internal_step2_sums"), _hook("fattn_internal_sum_shift")
     x, dout, qkv, g = seeded_qkv(orc, 64, 6, 240, 5, cuda)
     res = {}
-    for on in (1, 0, 1, 0, 1, 0):
-        prev = f(on)
+    modes = [(1, 0), (0, 0)] * 3 + ([(1, 3), (1, 3)] if not causal else [])
+    for on, sh in modes:
+        prev, prev_sh = sums(on), shift(sh)
         try:
             _, grad = run("fused_qkv", qkv, g, 6, 64, causal, 0.125)
         finally:
-            f(prev)
+            sums(prev)
+            shift(prev_sh)
         b = bits(grad)
-        if on in res:
-            assert torch.equal(b, res[on]), f"step 2 sums {'on' if on else 'off'}: reruns differ"
-        res[on] = b
-    say(f"  causal={causal}: step 2 sums on == off: {torch.equal(res[1], res[0])}")
-    assert torch.equal(res[1], res[0])
+        key = (on, sh)
+        if key in res:
+            assert torch.equal(b, res[key]), f"step 2 sums {key}: reruns differ"
+        res[key] = b
+    for key, b in res.items():
+        say(f"  causal={causal}: sums/shift {key} == step 3 alone: {torch.equal(b, res[(0, 0)])}")
+        assert torch.equal(b, res[(0, 0)]), key
 
 
 @pytest.mark.parametrize("d", [32, 64])
-def test_causal_dq_sums_match_turns(orc, cuda, d):
-    """Causal split backward with 8 | b h (step 2's last workgroups sum the dQ tiles, each waiting
-    only for the key blocks its tiles need) against the turn hand-over, which sums dQ in place in
-    the same key-block order: O and the whole gradient bit-identical, and within the fp64 bar."""
-    b, h, s = 2, 4, 200
+def test_step2_sums_across_xcds(orc, cuda, d):
+    """Every non-causal sum reading partials from another XCD (the shift hook, each of 1..7) at b 2
+    h 16 s 300: the gradient equals step 3's sums bit for bit, and after step 2 alone every tile's
+    done flag holds the launch's epoch (step 2 summed it)."""
+    sums, shift = _hook("fattn_internal_step2_sums"), _hook("fattn_internal_sum_shift")
+    h, s = 16, 300
+    x, dout, qkv, g = seeded_qkv(orc, 2, h, s, 40 + d, cuda, d=d)
+    prev = sums(0)
+    try:
+        _, want = run("fused_qkv", qkv, g, h, d, False, 0.125)
+    finally:
+        sums(prev)
+    for sh in range(1, 8):
+        prev_sh = shift(sh)
+        try:
+            _, grad = run("fused_qkv", qkv, g, h, d, False, 0.125)
+            summed = step2_summed_tiles(qkv, g, h, d, False, want)
+        finally:
+            shift(prev_sh)
+        say(f"  d{d} shift {sh}: equal {torch.equal(bits(grad), bits(want))}, "
+            f"step 2 summed {int(summed.sum())} of {summed.size}")
+        assert torch.equal(bits(grad), bits(want)), f"shift {sh}"
+        assert summed.all(), f"shift {sh}"
+
+
+@pytest.mark.parametrize("h,causal,final", [(8, False, True), (9, False, False), (6, True, True),
+                                            (5, True, True)])
+def test_step3_runs_only_where_needed(orc, cuda, h, causal, final):
+    """fattn_bwd_f32 with a split workspace, eager: where step 2's sums cover every tile (non-causal
+    b 1 h 8 at s 240: a whole number of heads per XCD; causal: always) no step 3 follows, so the
+    done flags keep the launch's epoch; elsewhere (non-causal h 9: the ninth head's key blocks
+    straddle XCDs, so the plan leaves it) step 3 runs and clears them. The gradient equals the
+    kernel-level steps 1-3 bit for bit either way."""
+    b, s, d = 1, 240, 64
+    x, dout, qkv, g = seeded_qkv(orc, b, h, s, 60 + h, cuda)
+    L = _lib.lib()
+    P = _p
+    st = _lib.arr([s * 3 * h * d, d, 3 * h * d])
+    gst = _lib.arr([s * h * d, d, h * d])
+    qp, kp, vp = (ctypes.c_void_p(qkv.data_ptr() + i * h * d * 4) for i in range(3))
+    stream = _st(qkv)
+    o = torch.empty(b, s, h * d, device=cuda)
+    lse = torch.empty(b, h, s, device=cuda)
+    _lib.check(L.fattn_fwd_f32(qp, kp, vp, P(o), P(lse), b, h, s, d, 0.125, int(causal), st, st,
+                               st, stream))
+    lay = ws_layout(b, h, s, d)
+    n = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
+    ws = torch.zeros(n, dtype=torch.uint8, device=cuda)
+    dqkv = torch.empty_like(qkv)
+    _lib.check(L.fattn_bwd_f32(qp, kp, vp, P(o), P(g), P(lse), P(dqkv), P(ws), n, b, h, s, d,
+                               0.125, int(causal), st, st, st, gst, stream))
+    torch.cuda.synchronize()
+    raw = ws.cpu().numpy()
+    ntile = -(-s // 16)
+    done = raw[lay["done"]:lay["done"] + b * h * ntile * 8].view(np.uint64)
+    epoch = raw[lay["epoch"]:lay["epoch"] + 8].view(np.uint64)[0]
+    say(f"  h{h} causal={causal}: done flags at the epoch {int((done == epoch).sum())} of "
+        f"{done.size}, zero {int((done == 0).sum())}")
+    if final:
+        assert epoch != 0 and (done == epoch).all(), "step 3 ran, or step 2 left tiles"
+    else:
+        assert (done == 0).all(), "step 3 did not clear the flags"
+    _, want = run("fused_qkv", qkv, g, h, d, causal, 0.125)
+    summed_want = step2_summed_tiles(qkv, g, h, d, causal, want)
+    assert torch.equal(bits(dqkv), bits(want))
+    assert summed_want.all() == final
+
+
+@pytest.mark.parametrize("d,b,h", [(32, 2, 4), (64, 2, 4), (64, 1, 6), (32, 3, 3)])
+def test_causal_dq_sums_match_turns(orc, cuda, d, b, h):
+    """Causal split backward (every key block sums the dQ tiles it completes, waiting only for the
+    key blocks those tiles need; at b h 6 or 9 those run on other XCDs) against the turn
+    hand-over, which sums dQ in place in the same key-block order: O and the whole gradient
+    bit-identical, and within the fp64 bar."""
+    s = 200
     rng = np.random.default_rng(5 + d)
     x = rng.standard_normal((b, s, 3 * h * d)).astype(np.float32)
     w = rng.standard_normal((b, s, h * d)).astype(np.float32)
@@ -851,7 +931,7 @@ def test_causal_dq_sums_match_turns(orc, cuda, d):
     check_errors(orc, o1, g1, ref_out, ref_grad, f"causal d{d}")
     summed = step2_summed_tiles(qkv, wt, h, d, True, g1)
     say(f"  step 2 summed {int(summed.sum())} of {summed.size} tiles")
-    assert summed.all(), "causal, 8 | b h: step 2 sums every tile"
+    assert summed.all(), "causal: step 2 sums every tile"
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -862,7 +942,7 @@ def test_graph_replays(orc, cuda, causal):
     backward leaves the sums' state clear (with stale state, a replay's sums would take the
     previous replay's partials). Eager work (new inputs, an eager run on the same workspace) and
     synchronisations run between the replays."""
-    b, h, s, d = 8, 6, 240, 64  # 8 divides b h: step 2 sums dQ tiles, causal too
+    b, h, s, d = 8, 6, 240, 64  # step 2 sums every dQ tile, causal too
     L = _lib.lib()
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     qkv = torch.empty(b, s, 3 * h * d, device=cuda)
