@@ -111,15 +111,15 @@ int fattn_bwd_main_f32(const float* q, const float* k, const float* v, const flo
 
 /* Backward step 3: with a split-size workspace, dQ = scale * (sum of step 2's partials in
  * key-block order) into part 0 of dqkv, for every query tile the last step 2 launch on this
- * workspace did not sum itself (its last workgroups sum the tiles whose contributing key blocks
- * all ran on their XCD; d <= 64; the same operations in the same order, so the result
- * does not depend on which kernel summed a tile); with a smaller workspace nothing to do (returns
- * 0). Has no counterpart launch in the reference (its dQ is summed in place, as the turn mode
- * here). */
+ * workspace did not sum itself (its last workgroups sum the tiles the schedule gives them; the
+ * same operations in the same order, so the result does not depend on which kernel summed a
+ * tile), then it clears the sums' flags; with a smaller workspace nothing to do (returns 0). Has
+ * no counterpart launch in the reference (its dQ is summed in place, as the turn mode here). */
 int fattn_bwd_dq_f32(float* dqkv, void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                      int64_t s, int64_t d, float scale, int causal, void* stream);
 
-/* All backward steps. Replaces cuda::backward (src/cuda.rs:187-260). */
+/* All backward steps. Replaces cuda::backward (src/cuda.rs:187-260). Step 3 is launched only
+ * where step 2's sums may leave tiles, or while `stream` is capturing a HIP graph. */
 int fattn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
                   const float* d_o, const float* lse, float* dqkv, void* workspace,
                   size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,
