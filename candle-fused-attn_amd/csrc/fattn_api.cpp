@@ -755,10 +755,10 @@ int fattn_backward(const float* q, int64_t q_offset, const int64_t q_shape[4],
 // kernel runs (fattn_internal.h). A summing unit is a workgroup appended to step 2's grid
 // (non-causal) or a key block's own workgroup summing its diagonal tiles (causal). out[0]:
 // workgroups appended to step 2's grid; out[1]: summing units with tiles to sum; out[2]:
-// violations -- a unit waits for a key block later in the grid, a non-causal unit for one that
-// xcd_remap puts on another XCD (the plan's dispatch order), a causal unit sums a tile it is not
-// the last contributor of, xcd_remap and item_xcd disagree, or a workgroup past the plan's range
-// has a target; out[3]: query tiles two units would both sum;
+// violations -- a causal unit waits for a key block later in the grid or sums a tile it is not
+// the last contributor of, a non-causal unit of XCD x takes a (b, h) whose last key block
+// xcd_remap does not put on x (or, past the XCDs' ranges, one that is not dealt round robin),
+// xcd_remap and item_xcd disagree, or a workgroup past the plan's range has a target; out[3]: query tiles two units would both sum;
 // out[4]: query tiles summed; out[5]: keys per key block (bwd_split_keys).
 int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int causal,
                              int64_t out[6]) {
@@ -823,9 +823,13 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
       ++targets;
       const int j1 = std::min(ntile, j0 + fattn::kSumTiles);
       // Key block kb of (b, h) bh: the (b, h)-major item bh nkb + kb under xcd_remap; summing
-      // workgroups come after every key block in the grid.
-      for (int kb = 0; kb < need_of(j1); ++kb) {
-        if (fattn::item_xcd(bh * nkb + kb, total) != x) ++bad;
+      // workgroups come after every key block in the grid. The first mc nchunk of each XCD take
+      // (b, h)s whose last key block runs on that XCD, the rest (b, h)s whose last key block is
+      // one of those dealt round robin.
+      const int last = bh * nkb + nkb - 1;
+      if (m < plan.mc * plan.nchunk ? fattn::item_xcd(last, total) != x
+                                    : last < (total & ~7)) {
+        ++bad;
       }
       mark(bh, j0, j1);
     }

@@ -81,35 +81,65 @@ __host__ __device__ inline int item_xcd(int item, int total) {
   return item >= full ? (item & 7) : item / (full >> 3);
 }
 
-// The dQ sums in step 2. Non-causal: `per` (b, h)s per XCD have every key block on that XCD (the
-// (b, h)-major key blocks under xcd_remap, when F is a whole number of (b, h)s), and the
-// workgroups appended for XCD x sum those, in the order their key blocks were dispatched (the
-// partials are read at device scope, so the XCD is not needed for correctness, only for that
-// order); causal: per = 1, every key block sums the tiles it completes. per = 0: no sums (step 3
-// sums every tile). nchunk = chunks of kSumTiles query tiles per (b, h) (non-causal).
+// The dQ sums in step 2 (split). Non-causal: workgroups appended to step 2's grid; workgroup
+// n_main + 8 m + x runs on XCD x (workgroups go to the XCDs round robin on MI355X). xcd_remap
+// gives XCD x the (b, h)-major key blocks [x F, (x + 1) F), F = floor(nkb b h / 8), and deals the
+// rest (fewer than 8) round robin. Summing workgroup m < mc nchunk of XCD x takes chunk
+// m % nchunk of the (m / nchunk)-th (b, h) whose last key block is among XCD x's, so that the
+// sums dispatched first wait for the key blocks dispatched first; the workgroups after those take,
+// in (b, h) order, the (b, h)s whose last key block is among the rest. Causal: every key block
+// sums the tiles it completes. The partials are read at device scope, so the XCDs order the waits
+// but are not needed for correctness. on = 0: no sums (step 3 sums every tile).
 struct SumPlan {
-  int per, nchunk;
+  int on;
+  int nchunk;  // chunks of kSumTiles query tiles per (b, h)
+  int nkb;     // key blocks per (b, h)
+  int mc;      // (non-causal) the most (b, h)s one XCD's range holds
 };
+// The (b, h)s whose last key block lies in XCD x's range of key blocks: lo .. hi (empty if
+// hi < lo); consecutive over x, from 0 to 8 F / nkb - 1.
+__host__ __device__ inline int sum_range_lo(int x, int F, int nkb) {
+  return (x * F + nkb) / nkb - 1;  // ceil((x F + 1) / nkb) - 1
+}
+__host__ __device__ inline int sum_range_hi(int x, int F, int nkb) { return (x + 1) * F / nkb - 1; }
 __host__ __device__ inline SumPlan sum_plan(int BH, int nkb, int ntile, int d, int causal) {
-  SumPlan p{0, (ntile + kSumTiles - 1) / kSumTiles};
+  SumPlan p{0, (ntile + kSumTiles - 1) / kSumTiles, nkb, 0};
   // (At d 128 the split kernel has the non-causal tail sums only.)
   if ((d > 64 && causal) || nkb > kSumMaxBlocks || BH <= 0) return p;
-  if (causal) {
-    p.per = 1;  // (a flag: every key block sums the tiles it completes)
-  } else {
-    const int f = ((nkb * BH) & ~7) >> 3;
-    p.per = f > 0 && f % nkb == 0 ? f / nkb : 0;
+  p.on = 1;
+  if (!causal) {
+    const int F = nkb * BH / 8;
+    for (int x = 0; x < 8; ++x) {
+      const int n = sum_range_hi(x, F, nkb) - sum_range_lo(x, F, nkb) + 1;
+      p.mc = n > p.mc ? n : p.mc;
+    }
   }
   return p;
 }
-// Non-causal summing workgroup m of XCD x (workgroup n_main + 8 m + x): the (b, h) it sums (XCD
-// x's (b, h)s one after the other) and its first query tile. False for a workgroup with nothing
-// to sum (m past the plan; never a (b, h) >= BH), and always when causal (no summing workgroups).
+// Workgroups appended to step 2's grid for the non-causal sums (a multiple of 8).
+__host__ __device__ inline int sum_blocks(SumPlan p, int BH, int causal) {
+  if (causal || !p.on) return 0;
+  const int left = BH - 8 * (p.nkb * BH / 8) / p.nkb;
+  return 8 * p.mc * p.nchunk + (left * p.nchunk + 7) / 8 * 8;
+}
+// Non-causal summing workgroup m of XCD x (workgroup n_main + 8 m + x): the (b, h) it sums and
+// its first query tile. False for a workgroup with nothing to sum (past the plan or past b h),
+// and always when causal (no summing workgroups).
 __host__ __device__ inline bool sum_target(SumPlan p, int x, int m, int BH, int causal, int* bh,
                                            int* j0) {
-  if (causal || p.per <= 0 || m >= p.per * p.nchunk) return false;
-  *bh = x * p.per + m / p.nchunk;
-  *j0 = m % p.nchunk * kSumTiles;
+  if (causal || !p.on) return false;
+  const int F = p.nkb * BH / 8;
+  if (m < p.mc * p.nchunk) {
+    const int b0 = sum_range_lo(x, F, p.nkb) + m / p.nchunk;
+    if (b0 > sum_range_hi(x, F, p.nkb) || b0 >= BH) return false;
+    *bh = b0;
+    *j0 = m % p.nchunk * kSumTiles;
+    return true;
+  }
+  const int idx = (m - p.mc * p.nchunk) * 8 + x, left0 = 8 * F / p.nkb;
+  if (idx >= (BH - left0) * p.nchunk) return false;
+  *bh = left0 + idx / p.nchunk;
+  *j0 = idx % p.nchunk * kSumTiles;
   return *bh < BH;
 }
 // Keys per key block of the split step 2 (d <= 64): kBwdKeys, or twice that (each wave owning two

@@ -1329,17 +1329,16 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // results are bit-identical whichever kernel sums a tile), stored from fragment order straight
 // into dQ rows (16 lanes write 64 contiguous bytes). Then the tiles' done flags (the epoch), which
 // step 3 checks when it runs: after a kernel-level step 2, while a graph is captured (step 3 also
-// clears the flags a replay, with the same epoch, must not see), or where the plan leaves tiles.
+// clears the flags a replay, with the same epoch, must not see), or where no sums are planned.
 // Otherwise no step 3 follows (sums_final): a wait then gives up only after kSumPollsFinal polls
-// (about half a second), raising the guard word and writing NaN into the tiles' rows; with step 3
-// to follow it gives up after kSumPolls and leaves the tiles to step 3.
+// (about a second), raising the guard word and writing NaN into the tiles' rows; with step 3 to
+// follow it gives up after kSumPolls and leaves the tiles to step 3.
 // Who sums:
 //   non-causal: workgroups appended to step 2's grid (in-order dispatch starts them only once every
-//   key block has been dispatched). Workgroup n_main + 8 m + x (on XCD x: workgroups go to the
-//   XCDs round robin on MI355X) sums chunk m of the query tiles of the (b, h)s whose key blocks
-//   xcd_remap put on XCD x (sum_target: plan.per (b, h)s per XCD, kSumTiles tiles per chunk, in the
-//   order their key blocks were dispatched, so the earliest sums wait for the earliest key blocks;
-//   the host sizes the grid from the same plan);
+//   key block has been dispatched), kSumTiles query tiles each, every tile of every (b, h): those
+//   on XCD x first take the (b, h)s whose last key block xcd_remap put on XCD x, in the order
+//   their key blocks were dispatched, so the earliest sums wait for the earliest key blocks
+//   (sum_plan / sum_target; the host sizes the grid from the same plan);
 //   causal: key block kb's own workgroup, after its walk, sums the tiles whose last contributor it
 //   is (own_tiles: its diagonal tiles 4 kb .. 4 kb + 3), which need key blocks 0 .. kb, whose
 //   workgroups kb' b h + bh come earlier in the grid. No workgroup is appended: a tile is summed as
@@ -1349,8 +1348,8 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 // Every poll ends: the key blocks waited for have smaller workgroup numbers, so they were
 // dispatched before the polling workgroup and run to completion whatever it does.
 // kSumTiles query tiles per summing workgroup: at config 2, 1, 2 or 15 were slower and 4 the same.
-constexpr int kSumPolls = 4096;
-constexpr int kSumPollsFinal = 1 << 20;
+constexpr int kSumPolls = 4096;       // about 14 ms
+constexpr int kSumPollsFinal = 1 << 18;  // about 0.9 s
 template <int D, int NT>
 __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, int j1,
                                               unsigned* flag) {
@@ -1374,7 +1373,13 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
         all = true;
         break;
       }
-      __builtin_amdgcn_s_sleep(16);  // about 1000 cycles between polls
+      // About 1000 cycles between polls, 8000 after the first 256 (a sum dispatched while its
+      // key blocks still have long to run: where they do not fill the chip).
+      if (it < 256) {
+        __builtin_amdgcn_s_sleep(16);
+      } else {
+        __builtin_amdgcn_s_sleep(127);
+      }
     }
     if (tid == 0) *flag = all ? 1u : 0u;
     if (tid == 0 && !all && a.sums_final) {
@@ -1995,14 +2000,14 @@ bool step2_sums_of(int64_t nbh, int64_t s, int d, int causal, int keys) {
   // The range check keeps b h s (hence every count below) inside int32.
   const int nkb = static_cast<int>((s + keys - 1) / keys);
   const int ntile = static_cast<int>((s + kQT - 1) / kQT);
-  return sum_plan(static_cast<int>(nbh), nkb, ntile, d, causal).per > 0;
+  return sum_plan(static_cast<int>(nbh), nkb, ntile, d, causal).on != 0;
 }
 int64_t sum_blocks_of(int64_t nbh, int64_t s, int d, int causal, int keys) {
   if (causal || !step2_sums_of(nbh, s, d, causal, keys)) return 0;
   const int nkb = static_cast<int>((s + keys - 1) / keys);
   const int ntile = static_cast<int>((s + kQT - 1) / kQT);
   const SumPlan p = sum_plan(static_cast<int>(nbh), nkb, ntile, d, causal);
-  return int64_t{8} * p.per * p.nchunk;
+  return sum_blocks(p, static_cast<int>(nbh), causal);
 }
 int64_t dq_grid_of(int64_t nbh, int64_t s, int d, int causal, int keys) {
   const int64_t tiles = bwd_dq_blocks(1, nbh, s);
@@ -2012,12 +2017,9 @@ int64_t dq_grid_of(int64_t nbh, int64_t s, int d, int causal, int keys) {
 }
 }  // namespace
 bool bwd_step2_sums_all(int64_t nbh, int64_t b, int64_t h, int64_t s, int d, int causal) {
+  // The plan, where on, gives every query tile of every (b, h) to one summing unit.
   const int keys = d <= 64 ? bwd_split_keys(b, h, s, d, causal) : kBwdKeys;
-  if (!step2_sums_of(nbh, s, d, causal, keys)) return false;
-  const int nkb = static_cast<int>((s + keys - 1) / keys);
-  const int ntile = static_cast<int>((s + kQT - 1) / kQT);
-  const SumPlan p = sum_plan(static_cast<int>(nbh), nkb, ntile, d, causal);
-  return causal ? p.per > 0 : int64_t{8} * p.per == nbh;
+  return step2_sums_of(nbh, s, d, causal, keys);
 }
 bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal) {
   return step2_sums_of(b * h, s, d, causal, bwd_split_keys(b, h, s, d, causal));

@@ -119,7 +119,7 @@ int fattn_bwd_dq_f32(float* dqkv, void* workspace, size_t workspace_bytes, int64
                      int64_t s, int64_t d, float scale, int causal, void* stream);
 
 /* All backward steps. Replaces cuda::backward (src/cuda.rs:187-260). Step 3 is launched only
- * where step 2's sums may leave tiles, or while `stream` is capturing a HIP graph. */
+ * where step 2 has no dQ sums, or while `stream` is capturing a HIP graph. */
 int fattn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
                   const float* d_o, const float* lse, float* dqkv, void* workspace,
                   size_t workspace_bytes, int64_t b, int64_t h, int64_t s, int64_t d,

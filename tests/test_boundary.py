@@ -321,27 +321,37 @@ def expected_keys(bh, s, d, causal):
 
 
 def expected_sum_bh(bh, s, causal, keys=64):
-    """Restated from the schedule's definition. Non-causal: the (b, h)s whose key blocks all run
-    on one XCD when workgroups go to the 8 XCDs round-robin -- (b, h)-major key blocks under
-    xcd_remap, XCD x holding items [x F, (x + 1) F), F = floor(nkb b h / 8): a whole number of
-    (b, h)s per XCD or no sums; causal: every (b, h) (the partials are read at device scope, so a
-    key block sums its tiles whatever XCDs its contributors ran on)."""
+    """Restated from the schedule's definition: every (b, h) has its tiles summed in step 2 while
+    a (b, h) has at most 256 key blocks (the summing units read the partials at device scope, so
+    where the key blocks ran does not matter)."""
     nkb = -(-s // keys)
-    if nkb > 256:
-        return 0
-    if causal:
-        return bh
-    f = (nkb * bh) // 8
-    return 8 * (f // nkb) if f > 0 and f % nkb == 0 else 0
+    return 0 if nkb > 256 else bh
+
+
+def expected_sum_grid(bh, s, keys=64):
+    """Non-causal summing workgroups appended to step 2's grid, restated: XCD x's range of the
+    (b, h)-major key blocks is [x F, (x + 1) F), F = floor(nkb b h / 8); each XCD's first mc nchunk
+    workgroups take the (b, h)s whose last key block is in its range (mc: the most any range
+    holds), then the (b, h)s whose last key block lies past 8 F take nchunk workgroups each, padded
+    to a multiple of 8."""
+    nkb, ntile = -(-s // keys), -(-s // 16)
+    nchunk = -(-ntile // 3)
+    f = nkb * bh // 8
+    lasts = [(b_ * nkb + nkb - 1) for b_ in range(bh)]
+    counts = [sum(1 for last in lasts if x * f <= last < (x + 1) * f) for x in range(8)]
+    left = sum(1 for last in lasts if last >= 8 * f)
+    return 8 * max(counts) * nchunk + -(-left * nchunk // 8) * 8
 
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_step2_dq_sum_schedule(causal):
     """Step 2's dQ sums, over many shapes (the kernel's own scheduling functions, run on the
-    host): every key block a summing unit waits for comes earlier in the grid (and, non-causal,
-    runs on that unit's XCD: the plan's order), no target lies past b h (the case a rounded-up per-XCD count once produced: nkb = 1, b h
-    not a multiple of 8, e.g. h 17 s 50), no tile is summed twice, and exactly the (b, h)s the
-    schedule's definition sums are summed, every one of their tiles.
+    host): a causal unit waits only for key blocks earlier in the grid; a non-causal unit of XCD x
+    takes a (b, h) whose last key block runs on x (or, after those, one whose last key block is
+    dealt round robin: the plan's order); no target lies past b h (the case a rounded-up per-XCD
+    count once produced: nkb = 1, b h not a multiple of 8, e.g. h 17 s 50); no tile is summed
+    twice; every tile of every (b, h) is summed (up to 256 key blocks per (b, h)), by the
+    restated number of appended workgroups.
     Non-causal, the units are workgroups appended to the grid, ceil(ntile / 3) per (b, h) (every
     head_dim); causal, every key block's own workgroup sums its diagonal tiles (none appended; d 64
     and below: step 3 sums them at d 128)."""
@@ -361,14 +371,16 @@ def test_step2_dq_sum_schedule(causal):
                     assert a["grid"] == 0 and a["targets"] == want_bh * nkb, (s, bh, d, a)
                 else:
                     nchunk = -(-ntile // 3)
-                    assert a["grid"] == want_bh * nchunk and a["targets"] == a["grid"], \
-                        (s, bh, d, a)
+                    assert a["targets"] == want_bh * nchunk, (s, bh, d, a)
+                    want_grid = expected_sum_grid(bh, s, keys) if want_bh else 0
+                    assert a["grid"] == want_grid, (s, bh, d, a, want_grid)
                 n += 1
     assert n > 1000
-    # The advisor's case: b 1, h 17, s 50 (one key block per (b, h)): 16 heads summed in step 2.
+    # The advisor's case: b 1, h 17, s 50 (one key block per (b, h)): no target past b h; all 17
+    # heads summed in step 2 (16 by the XCDs' ranges, the 17th by the round-robin rest).
     if not causal:
         a = sum_audit(1, 17, 50, 64, False)
-        assert a["covered"] == 16 * 4 and a["bad"] == 0
+        assert a["covered"] == 17 * 4 and a["bad"] == 0
         # The benchmark's shapes: config 2 (s 240) keeps 64-key blocks, config 5 (s 1024) 128.
         assert sum_audit(64, 6, 240, 64, False)["keys"] == 64
         assert sum_audit(16, 16, 1024, 64, False)["keys"] == 128
