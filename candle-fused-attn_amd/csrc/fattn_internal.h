@@ -104,8 +104,7 @@ __host__ __device__ inline int sum_range_lo(int x, int F, int nkb) {
 __host__ __device__ inline int sum_range_hi(int x, int F, int nkb) { return (x + 1) * F / nkb - 1; }
 __host__ __device__ inline SumPlan sum_plan(int BH, int nkb, int ntile, int d, int causal) {
   SumPlan p{0, (ntile + kSumTiles - 1) / kSumTiles, nkb, 0};
-  // (At d 128 the split kernel has the non-causal tail sums only.)
-  if ((d > 64 && causal) || nkb > kSumMaxBlocks || BH <= 0) return p;
+  if (nkb > kSumMaxBlocks || BH <= 0) return p;
   p.on = 1;
   if (!causal) {
     const int F = nkb * BH / 8;

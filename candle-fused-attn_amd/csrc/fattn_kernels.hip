@@ -819,8 +819,13 @@ __device__ __forceinline__ bool wait_turn(int* p, int want, int* guard) {
 // matrix cores idle behind barriers), 2 at D 128 (its registers do not fit 3).
 template <int D>
 __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, unsigned* flag);
+template <int D, int NT>
+__device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, int j1,
+                                              unsigned* flag);
 
-template <bool kSplit, int D>
+// kOwnSums (split, causal): each key block sums the dQ tiles it completes after its walk; a
+// separate instantiation, so that the non-causal kernel's registers are not spent on it.
+template <bool kSplit, int D, bool kOwnSums = false>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArgs a) {
   constexpr int kKR = D / 4;                  // K (or V) values per lane: B operands of S, dP
@@ -842,7 +847,7 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   __shared__ __attribute__((aligned(16))) float sL[2][kQT];
   __shared__ __attribute__((aligned(16))) float sD[2][kQT];
   __shared__ int s_item;
-  __shared__ unsigned s_flag;  // a dQ sum's poll result (split, non-causal)
+  __shared__ unsigned s_flag;  // a dQ sum's poll result (split)
 
   const int tid = threadIdx.x, lane = tid & 63, lo = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
@@ -860,9 +865,11 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
       return;
     }
     item = a.causal ? id : xcd_remap(id, n);
-    // No turn waits here: the guard word reads 0 (step 1, which clears it for the turn mode, does
-    // not run for the split mode).
-    if (id == 0 && tid == 0) a.ctrl[kCtrlGuard] = 0;
+    // No turn waits here: the guard word reads 0 (unless a final sum's wait gave up; written
+    // through, as that raise is, so that no copy of it lingers in this XCD's L2).
+    if (id == 0 && tid == 0) {
+      __hip_atomic_store(a.ctrl + kCtrlGuard, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   } else {
     // Ticket: the key block this workgroup computes, in arrival order. Key block kb of a (b, h)
     // has a later item than kb - 1, so the block it waits on was taken by an earlier, running
@@ -1298,6 +1305,14 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
     for (int mt = 0; mt < kDT; ++mt) {
       st4(row + part + 16 * mt + 4 * g, dka[mt] * a.scale);
       st4(row + 2 * part + 16 * mt + 4 * g, dva[mt]);
+    }
+  }
+  if constexpr (kSplit && kOwnSums) {
+    if (a.causal && a.arrive != nullptr) {
+      // The tiles whose last contributor is this key block (as bwd_split_kernel's).
+      int j0, j1;
+      own_tiles(kb, kBwdKeys, a.ntile, &j0, &j1);
+      bwd_sum_range<D, kBwdKeys / kQT>(a, bh, j0, j1, &s_flag);
     }
   }
 }
@@ -2091,8 +2106,9 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   if (d == 32) {
     fn = reinterpret_cast<const void*>(bwd_kernel<false, 32>);
   } else if (d == 128) {
-    fn = split ? reinterpret_cast<const void*>(bwd_kernel<true, 128>)
-               : reinterpret_cast<const void*>(bwd_kernel<false, 128>);
+    fn = !split  ? reinterpret_cast<const void*>(bwd_kernel<false, 128>)
+         : causal ? reinterpret_cast<const void*>(bwd_kernel<true, 128, true>)
+                  : reinterpret_cast<const void*>(bwd_kernel<true, 128>);
   } else {
     fn = reinterpret_cast<const void*>(bwd_kernel<false, 64>);
   }

@@ -363,8 +363,7 @@ def test_step2_dq_sum_schedule(causal):
                 keys = expected_keys(bh, s, d, causal)
                 assert a["keys"] == keys, (s, bh, d, a)
                 ntile, nkb = -(-s // 16), -(-s // keys)
-                # d 128: the non-causal tail sums only
-                want_bh = expected_sum_bh(bh, s, causal, keys) if d <= 64 or not causal else 0
+                want_bh = expected_sum_bh(bh, s, causal, keys)
                 assert a["bad"] == 0 and a["twice"] == 0, (s, bh, d, a)
                 assert a["covered"] == want_bh * ntile, (s, bh, d, a, want_bh)
                 if causal:

@@ -865,14 +865,24 @@ def test_step2_sums_across_xcds(orc, cuda, d):
 
 @pytest.mark.parametrize("d,h,causal,final", [(64, 8, False, True), (64, 9, False, True),
                                               (64, 6, True, True), (64, 5, True, True),
-                                              (128, 9, False, True), (128, 6, True, False)])
+                                              (128, 9, False, True), (128, 6, True, True),
+                                              (64, 9, False, False), (128, 5, True, False)])
 def test_step3_runs_only_where_needed(orc, cuda, d, h, causal, final):
-    """fattn_bwd_f32 with a split workspace, eager: where step 2's sums cover every tile (every
-    shape at d 64; non-causal at d 128) no step 3 follows, so the done flags keep the launch's
-    epoch; where they do not (causal d 128: step 2 sums nothing) step 3 runs and leaves the flags
-    zeroed. The gradient equals the kernel-level steps 1-3 bit for bit either way."""
+    """fattn_bwd_f32 with a split workspace, eager: where step 2 sums the dQ tiles (every shape
+    here) no step 3 follows, so the done flags keep the launch's epoch; with step 2's sums
+    switched off by the test hook (final False) step 3 runs and leaves the flags zeroed. The
+    gradient equals the kernel-level steps 1-3 bit for bit either way."""
     b, s = 1, 240
     x, dout, qkv, g = seeded_qkv(orc, b, h, s, 60 + h, cuda, d=d)
+    sums = _hook("fattn_internal_step2_sums")
+    prev = sums(1 if final else 0)
+    try:
+        _step3_case(orc, cuda, b, h, s, d, causal, final, qkv, g)
+    finally:
+        sums(prev)
+
+
+def _step3_case(orc, cuda, b, h, s, d, causal, final, qkv, g):
     L = _lib.lib()
     P = _p
     st = _lib.arr([s * 3 * h * d, d, 3 * h * d])
@@ -906,7 +916,8 @@ def test_step3_runs_only_where_needed(orc, cuda, d, h, causal, final):
         assert step2_summed_tiles(qkv, g, h, d, causal, want).all()
 
 
-@pytest.mark.parametrize("d,b,h", [(32, 2, 4), (64, 2, 4), (64, 1, 6), (32, 3, 3)])
+@pytest.mark.parametrize("d,b,h", [(32, 2, 4), (64, 2, 4), (64, 1, 6), (32, 3, 3), (128, 2, 4),
+                                   (128, 1, 6)])
 def test_causal_dq_sums_match_turns(orc, cuda, d, b, h):
     """Causal split backward (every key block sums the dQ tiles it completes, waiting only for the
     key blocks those tiles need; at b h 6 or 9 those run on other XCDs) against the turn
