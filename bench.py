@@ -17,7 +17,9 @@ configs 3-5, then W warm-up + K timed steps (`value`), K forwards (`fwd_ms`), K 
 steps (`kernels_us`, `roofline`), and last config 2 at head_dim 32 and 128. MI355X runs at
 lower clocks for some tens of milliseconds after an idle second, so the headline steps come right
 after sustained work, as in a training loop; the from-idle figure shows what a short run on an
-idle GPU sees.
+idle GPU sees. The K timed steps run back to back with HIP events only before the first, after
+the fifth, before the fifth-last and after the last (the means of the first and last 5 steps come
+from those); an event between every two steps would add its own time to each (about 2 us).
 
 Prints ONE JSON line. `--gpus N` with N > 1 exits: this build runs on one GPU.
 
@@ -195,20 +197,28 @@ class Workload:
         return flops(self.b, self.h, self.s, self.d, self.causal)
 
 
-def event_steps(torch, stream, fn, n):
-    """n calls of fn back to back, a HIP event on the launch stream before the first and after
-    each: (mean ms per call over all n, the per-call ms list, host wall ms per call)."""
+def event_steps(torch, stream, fn, n, edge=5):
+    """n calls of fn back to back, timed with HIP events on the launch stream: one before the first
+    call, one after the last, one after the first `edge` calls and one before the last `edge`, and
+    none between other calls (an event on the stream adds its own time to the call it follows:
+    about 2 us per fwd+bwd step at config 2). Returns (mean ms per call over all n, (mean ms of the
+    first `edge` calls, of the last `edge` calls), host wall ms per call)."""
+    e = max(1, min(edge, n))
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     t0 = time.perf_counter()
     ev[0].record(stream)
     for i in range(n):
+        if i == n - e:
+            ev[2].record(stream)
         fn()
-        ev[i + 1].record(stream)
+        if i == e - 1:
+            ev[1].record(stream)
+    ev[3].record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / n
-    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
-    return ev[0].elapsed_time(ev[n]) / n, per, wall
+    edges = (ev[0].elapsed_time(ev[1]) / e, ev[2].elapsed_time(ev[3]) / e)
+    return ev[0].elapsed_time(ev[3]) / n, edges, wall
 
 
 def kernel_steps(torch, stream, kernels, n):
@@ -454,10 +464,9 @@ def main() -> int:
     for _ in range(max(args.warmup, 1)):
         w.step()
     torch.cuda.synchronize()
-    cold_ms, cold_steps, _ = event_steps(torch, w.stream, w.step, K)
-    log(f"bench: from idle: fwd+bwd {cold_ms:.4f} ms (first {n5} steps "
-        f"{statistics.mean(cold_steps[:n5]):.4f}, last {n5} "
-        f"{statistics.mean(cold_steps[-n5:]):.4f})")
+    cold_ms, cold_edges, _ = event_steps(torch, w.stream, w.step, K, n5)
+    log(f"bench: from idle: fwd+bwd {cold_ms:.4f} ms (first {n5} steps {cold_edges[0]:.4f}, "
+        f"last {n5} {cold_edges[1]:.4f})")
 
     extra = {}
     if not args.no_extra:
@@ -480,12 +489,12 @@ def main() -> int:
     # Stop for an nsys capture range, examples/compare.rs:261-277); `rocprofv3 --marker-trace`
     # records them. torch.cuda.nvtx is roctx on ROCm.
     torch.cuda.nvtx.range_push("fattn timed fwd+bwd")
-    fwd_bwd_ms, per_step, fwd_bwd_wall = event_steps(torch, w.stream, w.step, K)
+    fwd_bwd_ms, edges, fwd_bwd_wall = event_steps(torch, w.stream, w.step, K, n5)
     torch.cuda.nvtx.range_pop()
     torch.cuda.nvtx.range_push("fattn timed fwd")
     fwd_ms, _, _ = event_steps(torch, w.stream, w.fwd, K)
     torch.cuda.nvtx.range_pop()
-    first5, last5 = statistics.mean(per_step[:n5]), statistics.mean(per_step[-n5:])
+    first5, last5 = edges
     log(f"bench: fwd+bwd {fwd_bwd_ms:.4f} ms (wall {fwd_bwd_wall:.4f}; first {n5} steps "
         f"{first5:.4f}, last {n5} {last5:.4f}), fwd {fwd_ms:.4f} ms")
 
@@ -545,8 +554,8 @@ def main() -> int:
         "fwd_bwd_first5_ms": round(first5, 5),
         "fwd_bwd_last5_ms": round(last5, 5),
         "fwd_bwd_from_idle_ms": round(cold_ms, 5),
-        "fwd_bwd_from_idle_first5_ms": round(statistics.mean(cold_steps[:n5]), 5),
-        "fwd_bwd_from_idle_last5_ms": round(statistics.mean(cold_steps[-n5:]), 5),
+        "fwd_bwd_from_idle_first5_ms": round(cold_edges[0], 5),
+        "fwd_bwd_from_idle_last5_ms": round(cold_edges[1], 5),
         "sequence": ("W warm-up + K timed steps from idle (fwd_bwd_from_idle_ms), "
                      + ("configs 3-5 timed (configs), " if extra else "")
                      + "W warm-up + K timed steps (value), K forwards, K kernel-level steps"
