@@ -31,16 +31,17 @@ struct View {
 };
 
 // Workspace of the backward, in this order, each part 256-byte aligned:
+//   ctrl   64 i32                           [0] key-block ticket, [32] guard word (first, so
+//                                           that its place does not depend on the shape)
 //   D      [b, h, s] f32                    rowsum(dO o O)
 //   turn   [b, h, ntile] i32                dQ turn counter per query tile (turn hand-over)
-//   ctrl   64 i32                           [0] key-block ticket, [32] guard word
 //   part   [nkb, b, h, ntile, kQT * d] f32 dQ partial per key block and query tile (split only)
 //   arrive [b, h, nkb] u64                  per key block: the epoch of the launch that finished
 //                                           it, or'ed with its XCD (split)
 //   done   [b, h, ntile] u64                the epoch of the launch whose step 2 summed the tile
 //   epoch  u64 (256 bytes)                  the epoch of the last step 2 launch on the workspace
-// with ntile = ceil(s / kBwdQueryTile), nkb = ceil(s / kBwdKeys). `bytes_min` covers D, turn and
-// ctrl (the turn hand-over), `bytes_split` all seven.
+// with ntile = ceil(s / kBwdQueryTile), nkb = ceil(s / kBwdKeys). `bytes_min` covers ctrl, D and
+// turn (the turn hand-over), `bytes_split` all seven.
 struct Workspace {
   size_t d_off, turn_off, ctrl_off, part_off, arrive_off, done_off, epoch_off, bytes_min,
       bytes_split;
@@ -48,14 +49,15 @@ struct Workspace {
 Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d);
 constexpr int kCtrlTicket = 0;
 constexpr int kCtrlGuard = 32;
-// dQ sums inside step 2 (split mode, d <= 64): a query tile is summed in step 2 once every key
-// block it needs has finished, if all of them ran on the XCD of the workgroup that sums it (their
-// partials are then in that XCD's L2 or written back from it, so it reads them coherently); step
-// 3 sums the rest. Non-causal, workgroups appended to step 2's grid do the sums; causal, each key
-// block's own workgroup sums, after its walk, the tiles whose last contributor it is. Every step 2 launch carries its own epoch (a 64-bit value unique to the launch, low 3
-// bits zero): the key blocks' arrivals and the done flags hold it, so nothing needs clearing
-// between launches and no stale or uninitialised value passes for a current one (but with a
-// 2^-64 chance). The summing workgroups poll at most kSumMaxBlocks arrival slots.
+// dQ sums inside step 2 (split mode): a query tile is summed in step 2 once every key block it
+// needs has finished, from partials stored and read at device scope (so whatever XCDs the key
+// blocks ran on); step 3, where it runs, sums what step 2 left. Non-causal, workgroups appended to
+// step 2's grid do the sums; causal, each key block's own workgroup sums, after its walk, the
+// tiles whose last contributor it is. Every step 2 launch carries its own epoch (a 64-bit value
+// unique to the launch, low 3 bits zero): the key blocks' arrivals and the done flags hold it, so
+// nothing needs clearing between launches and no stale or uninitialised value passes for a
+// current one (but with a 2^-64 chance). The summing workgroups poll at most kSumMaxBlocks
+// arrival slots.
 constexpr int kSumMaxBlocks = 256;
 constexpr int kSumTiles = 3;  // query tiles per summing workgroup
 // Causal: the query tiles whose last contributor is key block kb of `keys` keys (its diagonal
