@@ -41,9 +41,11 @@ Workspace workspace_layout(int64_t b, int64_t h, int64_t s, int64_t d) {
   return w;
 }
 
-// The split step 2's workgroup slots on gfx950 (256 CUs): 3 per CU with 64-key blocks, 2 with
-// 128-key blocks.
-int64_t split_slots(int keys) { return (keys > kBwdKeys ? 2 : 3) * int64_t{256}; }
+// The split step 2's workgroup slots on gfx950 (256 CUs): 3 per CU, 2 with 128-key blocks at
+// d 64.
+int64_t split_slots(int keys, int64_t d) {
+  return (keys > kBwdKeys && d > 32 ? 2 : 3) * int64_t{256};
+}
 
 // The (b, h) pairs per chunk of the split dQ sum that a workspace of ws_bytes holds: b h when it
 // holds the whole split; else, at d <= 64, from the most pairs whose split partials, arrival
@@ -71,7 +73,7 @@ int64_t split_chunk(int64_t b, int64_t h, int64_t s, int64_t d, size_t ws_bytes,
   }
   if (!causal) {
     const int keys = bwd_split_keys(b, h, s, static_cast<int>(d), 0);
-    const int64_t nkb = (s + keys - 1) / keys, slots = split_slots(keys);
+    const int64_t nkb = (s + keys - 1) / keys, slots = split_slots(keys, d);
     const int64_t quantum = slots / std::gcd(slots, nkb);
     if (lo >= quantum) lo -= lo % quantum;
     return lo == 0 || lo < min_pairs ? 0 : lo;
@@ -96,7 +98,7 @@ int64_t split_chunk(int64_t b, int64_t h, int64_t s, int64_t d, size_t ws_bytes,
 int64_t min_chunk_pairs(int64_t b, int64_t h, int64_t s, int64_t d, bool causal) {
   const int keys = bwd_split_keys(b, h, s, static_cast<int>(d), causal ? 1 : 0);
   const int64_t nkb = (s + keys - 1) / keys;
-  const int64_t blocks = (causal ? 4 : 1) * split_slots(keys);
+  const int64_t blocks = (causal ? 4 : 1) * split_slots(keys, d);
   return (blocks + nkb - 1) / nkb;
 }
 

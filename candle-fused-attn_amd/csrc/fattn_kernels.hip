@@ -1482,8 +1482,8 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
 }
 
 template <int D, int KG>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(KG == 1 ? BWD_WAVES : 2)))
-bwd_split_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(KG == 1 || D == 32 ? BWD_WAVES : 2))) bwd_split_kernel(BwdArgs a) {
   constexpr int kKeys = kBwdKeys * KG;
   static_assert(D <= 64, "D 128 has no LDS room for three buffers: bwd_kernel<true, 128>");
   static_assert(kNS == 1, "one 16-query subtile per tile");
@@ -1999,13 +1999,19 @@ bool set_step2_sums(bool on) { return g_step2_sums.exchange(on ? 1 : 0) != 0; }
 int set_sum_shift(int shift) { return g_sum_shift.exchange(shift & 7); }
 
 int bwd_split_keys(int64_t b, int64_t h, int64_t s, int d, int causal) {
-  // 128-key blocks (two 16-key groups per wave, 2 waves per SIMD): half the dQ partials and half
-  // the per-tile staging and barriers per product, against one wave per SIMD fewer. Measured
+  // 128-key blocks (two 16-key groups per wave): half the dQ partials and half the per-tile
+  // staging and barriers per product. At d 64 they hold 2 waves per SIMD instead of 3. Measured
   // (step 2, non-causal, d 64): s 384 +3.9 %, 512 -4.8 %, 768 -4.1 %, 1024 -6.7 %, 2048 -6.9 %,
   // 4096 -3.6 %; causal +1 to +31 % (the diagonal blocks' masked work doubles). They need two
-  // workgroups per CU to fill the chip.
-  if (d != 64 || causal || s < 512) return kBwdKeys;
-  return (s + 2 * kBwdKeys - 1) / (2 * kBwdKeys) * b * h >= 512 ? 2 * kBwdKeys : kBwdKeys;
+  // workgroups per CU to fill the chip. At d 32 they keep 3 waves per SIMD and pay where the
+  // halved workgroup count leaves fewer than two rounds of them (b h s 256 +8 %, 512 +60 %,
+  // config 2's shape -2 %); from two rounds on (1536 workgroups) they gain: b16 h16 s768 -3.4 %,
+  // s1024 -5.0 %, b8 h16 s2048 -4.4 %, b4 h16 s4096 -4.2 %.
+  const int64_t blocks128 = (s + 2 * kBwdKeys - 1) / (2 * kBwdKeys) * b * h;
+  if (causal) return kBwdKeys;
+  if (d == 32) return blocks128 >= 1536 ? 2 * kBwdKeys : kBwdKeys;
+  if (d != 64 || s < 512) return kBwdKeys;
+  return blocks128 >= 512 ? 2 * kBwdKeys : kBwdKeys;
 }
 namespace {
 // The schedule of a launch over nbh (b, h) pairs with key blocks of `keys` keys (a chunk's keys
@@ -2096,7 +2102,9 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
             arrive != nullptr && sums_final ? 1 : 0, g_sum_shift.load(std::memory_order_relaxed)};
   void* args[] = {&a};
   if (split && d <= 64) {
-    const void* fn = d == 32 ? reinterpret_cast<const void*>(bwd_split_kernel<32, 1>)
+    const void* fn = d == 32 ? (kkeys == kBwdKeys
+                                    ? reinterpret_cast<const void*>(bwd_split_kernel<32, 1>)
+                                    : reinterpret_cast<const void*>(bwd_split_kernel<32, 2>))
                      : kkeys == kBwdKeys ? reinterpret_cast<const void*>(bwd_split_kernel<64, 1>)
                                          : reinterpret_cast<const void*>(bwd_split_kernel<64, 2>);
     return static_cast<int>(launch(fn, nsum ? nmain + nsum : nblk, args, stream));

@@ -313,9 +313,12 @@ def sum_audit(b, h, s, d, causal):
 
 def expected_keys(bh, s, d, causal):
     """Keys per split key block, from the rule's definition: 128 (two 16-key groups per wave) for
-    non-causal d 64 from s 512 on when ceil(s / 128) b h >= 512 workgroups fill two per CU; else
-    64."""
-    if d == 64 and not causal and s >= 512 and -(-s // 128) * bh >= 512:
+    non-causal d 64 from s 512 on when ceil(s / 128) b h >= 512 workgroups fill two per CU, and
+    for non-causal d 32 when they make two rounds of three per CU (1536); else 64."""
+    blocks = -(-s // 128) * bh
+    if not causal and d == 64 and s >= 512 and blocks >= 512:
+        return 128
+    if not causal and d == 32 and blocks >= 1536:
         return 128
     return 64
 

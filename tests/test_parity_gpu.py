@@ -693,6 +693,30 @@ def test_long_noncausal_128_key_blocks(orc, cuda):
     assert torch.equal(bits(grad4), bits(grad))
 
 
+def test_d32_128_key_blocks(orc, cuda):
+    """Non-causal d 32 with at least 1536 workgroups of 128 keys (two rounds of three per CU)
+    runs 128-key blocks (bwd_split_kernel<32, 2>). At b 12 h 32 s 512: batch 0's 32 heads against
+    the fp64 oracle, two runs bit-identical, and step 2's own dQ sums switched off (step 3 sums
+    every tile) giving the same bits."""
+    from test_boundary import sum_audit
+    b, h, s, d = 12, 32, 512, 32
+    assert sum_audit(b, h, s, d, False)["keys"] == 128
+    x, dout, qkv, g = seeded_qkv(orc, b, h, s, 23, cuda, d=d)
+    say(f"d32 128-key blocks: b{b} h{h} s{s}")
+    out, grad = run("fused_qkv", qkv, g, h, d, False, 0.125)
+    ref_out, _, ref_grad = oracle_qkv(orc, x[:1], dout[:1], h, d, False, np.float64, 0.125)
+    check_errors(orc, out[:1], grad[:1], ref_out, ref_grad, "b12 h32 s512 d32, batch 0")
+    out2, grad2 = run("fused_qkv", qkv, g, h, d, False, 0.125)
+    assert torch.equal(bits(out2), bits(out)) and torch.equal(bits(grad2), bits(grad))
+    sums = _hook("fattn_internal_step2_sums")
+    prev = sums(0)
+    try:
+        _, grad3 = run("fused_qkv", qkv, g, h, d, False, 0.125)
+    finally:
+        sums(prev)
+    assert torch.equal(bits(grad3), bits(grad)), "step 2 sums off: different bits"
+
+
 def test_long_noncausal_128_key_blocks_sum_schedule(orc, cuda):
     """The 128-key path's dQ sums in step 2: b 1 h 128 s 512 with every head given the same q, k,
     v and output gradient, so that every head's O and gradient must be bit-identical whichever
