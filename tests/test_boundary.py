@@ -82,6 +82,11 @@ def test_workspace_size_is_aligned_and_monotone():
     assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 64)
             == L.fattn_bwd_workspace_split_bytes(1, 48, 4096, 64))
     assert L.fattn_bwd_workspace_split_bytes(1, 64, 4096, 64) > cap
+    # d 32, 32 MiB per pair: 127 fit, rounded to 120 (8 | chunk), so 2 chunks, made equal: 64, 64
+    # (each chunk's 64 x 32 key blocks of 128 keys fill the 768 workgroup slots several times)
+    assert L.fattn_bwd_workspace_split_bytes(8, 16, 4096, 32) > cap
+    assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 32)
+            == L.fattn_bwd_workspace_split_bytes(1, 64, 4096, 32))
     assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 128)
             == L.fattn_bwd_workspace_min_bytes(8, 16, 4096, 128))
 
