@@ -1270,17 +1270,20 @@ def test_very_long_sequence(orc, cuda, causal):
 
 # --- the split dQ sum by chunks of (b, h) (a workspace that holds some pairs' partials) ---------
 
-@pytest.mark.parametrize("causal", [False, True])
-def test_split_by_chunks_matches_whole(cuda, causal):
+@pytest.mark.parametrize("causal,d", [(False, 64), (True, 64), (False, 32)])
+def test_split_by_chunks_matches_whole(cuda, causal, d):
     """fattn_bwd_f32 with a workspace that holds the split partials of only some (b, h) pairs runs
     steps 2 and 3 per chunk of pairs (causal: equal, 8 | chunk; non-causal: whole rounds of slots), where the chunks are
     large enough to beat the turn hand-over (s 4096: 12 pairs non-causal, 48 causal): the
     gradient equals the whole split's bit for bit (each pair's arithmetic and summation order are
     the same), and the guard word reads 0. Non-causal b h 24 in chunks of 16 and 8; causal b h 96
-    in two of 48. A workspace whose chunks would be smaller takes the turn hand-over: causal, its
-    gradient equals the split's bit for bit too."""
-    b, h, s, d = (2, 12, 4096, 64) if not causal else (6, 16, 4096, 64)
+    in two of 48; d 32 (128-key blocks, three workgroups per CU) b h 48 in two of 24. A workspace
+    whose chunks would be smaller takes the turn hand-over: causal, its gradient equals the
+    split's bit for bit too."""
+    b, h, s = (2, 12, 4096) if not causal else (6, 16, 4096)
     pairs = 16 if not causal else 48
+    if d == 32:
+        b, h, s, pairs = 3, 16, 4096, 24
     L = _lib.lib()
     g = torch.Generator(device=cuda).manual_seed(7)
     qkv = torch.randn(b, s, 3 * h * d, generator=g, device=cuda)
