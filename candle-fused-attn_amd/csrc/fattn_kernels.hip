@@ -1403,22 +1403,20 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
   }
   __syncthreads();
   const int b = (a.bh0 + bh) / a.H, h = (a.bh0 + bh) % a.H, S = a.S;
-  const int64_t row_stride0 = static_cast<int64_t>(3) * a.H * D;
+  const int64_t row_stride = static_cast<int64_t>(3) * a.H * D;
+  float* const dq_bh =
+      a.dqkv + static_cast<int64_t>(b) * S * row_stride + static_cast<int64_t>(h) * D;
   if (*flag == 0u) {
     if (a.sums_final) {
       // No step 3 follows: the tiles' dQ rows get NaN (the failure shows in the output).
-      float* dq0 = a.dqkv + static_cast<int64_t>(b) * S * row_stride0 + static_cast<int64_t>(h) * D;
       for (int e = tid; e < (j1 - j0) * kQT * D; e += kThreads) {
         const int q = j0 * kQT + e / D;
-        if (q < S) dq0[q * row_stride0 + e % D] = __builtin_nanf("");
+        if (q < S) dq_bh[q * row_stride + e % D] = __builtin_nanf("");
       }
     }
     return;
   }
   const int64_t slot = static_cast<int64_t>(BH) * ntile * (kQT * D);
-  const int64_t row_stride = static_cast<int64_t>(3) * a.H * D;
-  float* const dq_bh =
-      a.dqkv + static_cast<int64_t>(b) * S * row_stride + static_cast<int64_t>(h) * D;
   // Thread i sums float4 i (and i + kThreads, ... at D 128) of each of the tiles, four key blocks
   // at a time: the loads of all the tiles for those key blocks are issued together, then added in
   // key-block order.
