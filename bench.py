@@ -14,7 +14,12 @@ forward+backward, and each kernel on its own.
 
 Order of the GPU work: W warm-up + K timed steps from an idle GPU (`fwd_bwd_from_idle_ms`),
 configs 3-5, then W warm-up + K timed steps (`value`), K forwards (`fwd_ms`), K kernel-level
-steps (`kernels_us`, `roofline`), and last config 2 at head_dim 32 and 128. MI355X runs at
+steps (`kernels_us`), K op-level backwards (`bwd_ms`), and last config 2 at head_dim 32 and 128.
+`roofline` prices the op-level backward and forward windows: at config 2 each call is one launch
+(step 2 alone, the forward kernel alone), so K calls back to back between two events give the
+kernel's average launch duration plus the dispatch gap between launches; the kernel-level
+steps, with an event between every two launches, add the gap between an event and the next
+dispatch (about 3 us) to each kernel and are reported beside them. MI355X runs at
 lower clocks for some tens of milliseconds after an idle second, so the headline steps come right
 after sustained work, as in a training loop; the from-idle figure shows what a short run on an
 idle GPU sees. The K timed steps run back to back with HIP events only before the first, after
@@ -299,11 +304,13 @@ def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
 
 def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
     """Per-kernel durations of the headline's GPU work, from a rocprofv3 --kernel-trace file of
-    `bench.py --warmup W --steps K` (same W and K): the K timed forward+backward steps and the K
-    kernel-level steps (whose average step-2 duration is `kernels_us.bwd_main`), and the first
-    K steps from idle. Configs 3-5 run the same kernel names, so the dispatches are split into
-    steps (a step starts at a forward launch) and config 2's steps picked by the forward's name
-    and grid; the headline's are the run of them after configs 3-5."""
+    `bench.py --warmup W --steps K` (same W and K): the K timed forward+backward steps, the K
+    op-level forwards and backwards (`fwd_ms`, `bwd_ms`, which price `roofline`), the K
+    kernel-level steps (`kernels_us`), and the first K steps from idle. Configs 3-5 run the same
+    kernel names, so the dispatches are split into steps (a step starts at a forward launch, or at
+    a step-2 launch in a step that already holds one) and config 2's steps picked by the forward's
+    name and grid; the headline's are the run of them after configs 3-5, and its K backwards the
+    K steps after that run."""
     rows = []
     with open(trace_csv, newline="") as f:
         for r in csv.DictReader(f):
@@ -318,8 +325,13 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
     b, h, s = CONFIGS[2][2], CONFIGS[2][3], CONFIGS[2][4]
     main_fwd = (KERNEL_NAMES["fwd"], ((s + 127) // 128) * b * h)
     steps_seq: list[list] = []
+
+    def step2(name):
+        return name.startswith(("bwd_split_kernel", "bwd_kernel"))
+
     for t, name, wgs, us in rows:
-        if name.startswith("fwd_kernel") or not steps_seq:
+        if (name.startswith("fwd_kernel") or not steps_seq
+                or (step2(name) and any(step2(n) for n, _, _ in steps_seq[-1]))):
             steps_seq.append([])
         steps_seq[-1].append((name, wgs, us))
     is_main = [st[0][0] == main_fwd[0] and st[0][1] == main_fwd[1] for st in steps_seq]
@@ -342,7 +354,9 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
         later = [r for r in runs if r[0] > 0 and r[1] - r[0] >= need]
         first = later[0][0] if later else len(steps_seq)
     timed = steps_seq[first + warmup:first + warmup + steps]
+    fwds = steps_seq[first + warmup + steps:first + warmup + 2 * steps]
     kern = steps_seq[first + warmup + 2 * steps:first + warmup + 3 * steps]
+    bwds = steps_seq[first + warmup + 3 * steps:first + warmup + 4 * steps]
     if len(timed) < steps or len(kern) < steps:
         print(f"bench.py: the trace holds no run of {need} config-2 steps after the other "
               "configs", file=sys.stderr)
@@ -362,7 +376,10 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
                   f"| {min(v):.1f} | {max(v):.1f} | {100 * sum(v) / total:.1f} % |")
 
     table(f"The {steps} timed forward+backward steps (after {warmup} warm-up steps)", timed)
-    table(f"The {steps} kernel-level steps (`kernels_us`, `roofline.achieved`)", kern)
+    table(f"The {steps} op-level forwards (`fwd_ms`, `roofline.fwd_kernel_achieved`)", fwds)
+    if len(bwds) == steps and all(step2(st[0][0]) for st in bwds):
+        table(f"The {steps} op-level backwards (`bwd_ms`, `roofline.achieved`)", bwds)
+    table(f"The {steps} kernel-level steps (`kernels_us`)", kern)
     if idle:
         table(f"The first {steps} steps from idle (after {warmup} warm-up steps; "
               "`fwd_bwd_from_idle_ms`)", idle)
@@ -370,20 +387,24 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
 
 
 def time_extra(torch, w: Workload, steps: int, warmup: int) -> dict:
-    """Op-level forward and forward+backward ms, and each kernel's us, of one extra config."""
+    """Op-level forward, backward and forward+backward ms, and each kernel's us, of one extra
+    config."""
     for _ in range(warmup):
         w.step()
     fb_ms, _, _ = event_steps(torch, w.stream, w.step, steps)
     f_ms, _, _ = event_steps(torch, w.stream, w.fwd, steps)
     kus = kernel_steps(torch, w.stream, w.kernels, steps)
+    b_ms, _, _ = event_steps(torch, w.stream, w.bwd, steps)
     f_fwd, f_bwd = w.flops()
     bwd_us = kus.get("bwd_prep", 0.0) + kus["bwd_main"] + kus.get("bwd_dq", 0.0)
     return {
         "workload": f"{w.kind} b{w.b} h{w.h} s{w.s} d{w.d} "
                     + ("causal" if w.causal else "non-causal")
                     + (f", inputs ~N(0, {w.std ** 2:g})" if w.std != 1.0 else ""),
-        "fwd_ms": round(f_ms, 5), "fwd_bwd_ms": round(fb_ms, 5),
+        "fwd_ms": round(f_ms, 5), "bwd_ms": round(b_ms, 5), "fwd_bwd_ms": round(fb_ms, 5),
         "fwd_bwd_tflops": round((f_fwd + f_bwd) / (fb_ms * 1e-3) / 1e12, 3),
+        "fwd_frac": round(f_fwd / (f_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "bwd_frac": round(f_bwd / (b_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
         "kernels_us": {k: round(v, 2) for k, v in kus.items()},
         "bwd_main_frac": round(f_bwd / (kus["bwd_main"] * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
         "bwd_steps_frac": round(f_bwd / (bwd_us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
@@ -509,6 +530,17 @@ def main() -> int:
     log(f"bench: kernels fwd {fwd_us:.1f} us, prep {prep_us:.1f} us, bwd main {main_us:.1f} us, "
         f"dq sum {dq_us:.1f} us ({'split' if w.split else 'turns'}); step {kus['step']:.1f} us")
 
+    # The op-level backward alone, K calls back to back with events only at the window's ends.
+    # With a split workspace at d <= 64 a call is one launch of step 2 (step 1 launches nothing,
+    # and step 2 sums every dQ tile), so the window's mean is step 2's average launch duration
+    # plus one dispatch gap; the forward window (`fwd_ms`) is the forward kernel's likewise.
+    torch.cuda.nvtx.range_push("fattn timed bwd")
+    bwd_ms, _, _ = event_steps(torch, w.stream, w.bwd, K)
+    torch.cuda.nvtx.range_pop()
+    one_launch = w.split and D <= 64
+    log(f"bench: op-level bwd {bwd_ms:.4f} ms"
+        + (" (one step-2 launch per call)" if one_launch else ""))
+
     if not args.no_extra:
         # The other head dims the kernels are built for, at the headline's shape: after the
         # headline (right before it, the heavier head_dim 128 work left the next 25 steps 4 %
@@ -526,6 +558,10 @@ def main() -> int:
     main_tflops = f_bwd / (main_us * 1e-6) / 1e12
     bwd_steps_tflops = f_bwd / ((prep_us + main_us + dq_us) * 1e-6) / 1e12
     fwdk_tflops = f_fwd / (fwd_us * 1e-6) / 1e12
+    bwd_tflops = f_bwd / (bwd_ms * 1e-3) / 1e12
+    # Step 2's rate: from the op-level backward window where a call is that one launch, else from
+    # the kernel-level events around it.
+    step2_tflops = bwd_tflops if one_launch else main_tflops
     traffic = traffic_entry()
 
     result = {
@@ -549,6 +585,7 @@ def main() -> int:
             "entry": "fattn_qkv_forward + fattn_qkv_backward",
         },
         "fwd_ms": round(fwd_ms, 5),
+        "bwd_ms": round(bwd_ms, 5),
         "fwd_bwd_ms": round(fwd_bwd_ms, 5),
         "fwd_bwd_wall_ms": round(fwd_bwd_wall, 5),
         "fwd_bwd_first5_ms": round(first5, 5),
@@ -558,7 +595,8 @@ def main() -> int:
         "fwd_bwd_from_idle_last5_ms": round(cold_edges[1], 5),
         "sequence": ("W warm-up + K timed steps from idle (fwd_bwd_from_idle_ms), "
                      + ("configs 3-5 timed (configs), " if extra else "")
-                     + "W warm-up + K timed steps (value), K forwards, K kernel-level steps"
+                     + "W warm-up + K timed steps (value), K forwards, K kernel-level steps, "
+                     + "K backwards"
                      + (", config 2 at d 32 / 128 timed (configs)" if extra else "")),
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_bwd_tflops": round(total_tflops, 3),
@@ -572,15 +610,21 @@ def main() -> int:
                        "workgroups sum dQ tiles)" if w.split
                        else "bwd_kernel<false, 64> (fattn_bwd_main_f32_d64, turns)"),
             "bound": "mfma",
-            "achieved": round(main_tflops, 3),
+            "achieved": round(step2_tflops, 3),
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(main_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+            "frac": round(step2_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             **traffic,
             "flops_per_launch": f_bwd,
+            "achieved_from": (f"bwd_ms: {K} op-level backwards back to back, one step-2 launch "
+                              "each, HIP events at the window's ends" if one_launch
+                              else "kernels_us.bwd_main: kernel-level events"),
+            "kernel_level_achieved": round(main_tflops, 3),
+            "kernel_level_frac": round(main_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             "bwd_steps_1_3_achieved": round(bwd_steps_tflops, 3),
-            "fwd_kernel_achieved": round(fwdk_tflops, 3),
-            "fwd_kernel_frac": round(fwdk_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+            "fwd_kernel_achieved": round(fwd_tflops, 3),
+            "fwd_kernel_frac": round(fwd_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+            "fwd_kernel_level_frac": round(fwdk_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
         },
     }
 
