@@ -1,6 +1,7 @@
-"""bench.py's kernel-trace summary (`--trace-from`) on a synthetic rocprofv3 kernel trace: it must
-pick the headline's windows out of a run that also launches configs 3-5 and the other head dims
-with kernels of the same names (CPU only; no GPU, no rocprofv3)."""
+"""bench.py's profile summaries on synthetic rocprofv3 files (CPU only; no GPU, no rocprofv3):
+the kernel-trace summary (`--trace-from`) must pick the headline's windows out of a run that also
+launches configs 3-5 and the other head dims with kernels of the same names, and the traffic
+summary (`--traffic-from`) must scale the counters by the copy's and go stale with the library."""
 import csv
 import subprocess
 import sys
@@ -71,3 +72,37 @@ def test_trace_windows(tmp_path):
     assert by[f"The {k} op-level backwards"] == {MAIN: (k, 137.0)}
     assert by[f"The {k} kernel-level steps"] == {MAIN: (k, 135.0), FWD: (k, 52.0), DQ: (k, 4.0)}
     assert by[f"The first {k} steps from idle"] == {MAIN: (k, 160.0), FWD: (k, 60.0)}
+
+
+def write_counters(path, counter, rows):
+    with open(path, "w", newline="") as f:
+        wr = csv.DictWriter(f, fieldnames=["Kernel_Name", "Counter_Name", "Counter_Value"])
+        wr.writeheader()
+        for name, value in rows:
+            wr.writerow({"Kernel_Name": name, "Counter_Name": counter, "Counter_Value": value})
+
+
+def test_traffic_summary_and_staleness(tmp_path, monkeypatch):
+    """`--traffic-from`: each kernel's mean counter, scaled by what the counter reads for the
+    256 MiB copy (FETCH_SIZE half the copied bytes: factor 2; WRITE_SIZE whole: factor 1); the
+    bench line reports the step-2 bytes only while the measured library is the loaded one."""
+    copy = "__amd_rocclr_copyBuffer"
+    main = f"{PREFIX}{MAIN}(fattn::BwdArgs)"
+    fwd = f"{PREFIX}{FWD}(fattn::FwdArgs)"
+    fetch, write = tmp_path / "fetch.csv", tmp_path / "write.csv"
+    write_counters(fetch, "FETCH_SIZE", [(copy, 131072.0), (fwd, 46000.0), (fwd, 46400.0),
+                                         (main, 100000.0), (main, 100002.0)])
+    write_counters(write, "WRITE_SIZE", [(copy, 262144.0), (fwd, 23000.0), (fwd, 23000.0),
+                                         (main, 200000.0), (main, 200000.0)])
+    monkeypatch.setattr(bench, "TRAFFIC", tmp_path / "traffic.json")
+    monkeypatch.setattr(bench, "lib_sha256", lambda: "aaaa")
+    assert bench.summarize_traffic(str(fetch), str(write)) == 0
+    t = bench.json.loads((tmp_path / "traffic.json").read_text())
+    assert (t["scale_fetch"], t["scale_write"]) == (2.0, 1.0)
+    assert t["fwd"]["fetch_bytes"] == 46200 * 1024 * 2 and t["fwd"]["write_bytes"] == 23000 * 1024
+    assert t["bwd_main_bytes"] == 100001 * 1024 * 2 + 200000 * 1024
+    assert t["lib_sha256"] == "aaaa"
+    assert bench.traffic_entry()["traffic"] == t["bwd_main_bytes"]
+    monkeypatch.setattr(bench, "lib_sha256", lambda: "bbbb")  # another library: stale
+    e = bench.traffic_entry()
+    assert e["traffic"] is None and e["traffic_stale_bytes"] == t["bwd_main_bytes"]
