@@ -62,6 +62,7 @@ LIB = REPO / "candle-fused-attn_amd" / "lib" / "libfattn.so"
 COPY_KIB = 256 * 1024            # the --calibrate-copy kernel moves 256 MiB each way
 KERNEL_NAMES = {"fwd": "fwd_kernel<64, 128, 32, 3>", "bwd_main": "bwd_split_kernel<64, 1>",
                 "bwd_dq": "dq_kernel<64>"}
+CAUSAL_FWD_NAME = "fwd_kernel<64, 64, 32, 3>"   # config 3's forward
 
 # The BASELINE.json configurations this bench times: (name, kind, b, h, s, causal, seed, std).
 CONFIGS = {
@@ -302,7 +303,7 @@ def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
     return 0
 
 
-def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
+def summarize_trace(trace_csv: str, warmup: int, steps: int, cfg: int = 2) -> int:
     """Per-kernel durations of the headline's GPU work, from a rocprofv3 --kernel-trace file of
     `bench.py --warmup W --steps K` (same W and K): the K timed forward+backward steps, the K
     op-level forwards and backwards (`fwd_ms`, `bwd_ms`, which price `roofline`), the K
@@ -322,8 +323,12 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
             rows.append((int(r["Start_Timestamp"]), name, wgs,
                          (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
     rows.sort()
-    b, h, s = CONFIGS[2][2], CONFIGS[2][3], CONFIGS[2][4]
-    main_fwd = (KERNEL_NAMES["fwd"], ((s + 127) // 128) * b * h)
+    # The headline's forward: config 2's non-causal kernel (128-query blocks), or with --causal
+    # config 3's (64-query blocks).
+    b, h, s = CONFIGS[cfg][2], CONFIGS[cfg][3], CONFIGS[cfg][4]
+    qb = 64 if CONFIGS[cfg][5] else 128
+    main_fwd = (CAUSAL_FWD_NAME if CONFIGS[cfg][5] else KERNEL_NAMES["fwd"],
+                ((s + qb - 1) // qb) * b * h)
     steps_seq: list[list] = []
 
     def step2(name):
@@ -358,7 +363,7 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int) -> int:
     kern = steps_seq[first + warmup + 2 * steps:first + warmup + 3 * steps]
     bwds = steps_seq[first + warmup + 3 * steps:first + warmup + 4 * steps]
     if len(timed) < steps or len(kern) < steps:
-        print(f"bench.py: the trace holds no run of {need} config-2 steps after the other "
+        print(f"bench.py: the trace holds no run of {need} config-{cfg} steps after the other "
               "configs", file=sys.stderr)
         return 1
 
@@ -443,7 +448,8 @@ def main() -> int:
     if args.traffic_from:
         return summarize_traffic(*args.traffic_from)
     if args.trace_from:
-        return summarize_trace(args.trace_from, max(args.warmup, 1), max(args.steps, 1))
+        return summarize_trace(args.trace_from, max(args.warmup, 1), max(args.steps, 1),
+                               3 if args.causal else 2)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
               "(the op shards over (batch, head) with no communication; see DESIGN.md)",

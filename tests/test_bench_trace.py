@@ -11,27 +11,32 @@ ROOT = Path(__file__).resolve().parents[1]
 sys.path.insert(0, str(ROOT))
 
 import bench  # noqa: E402
+import pytest  # noqa: E402
 
 PREFIX = "void fattn::(anonymous namespace)::"
 FWD, MAIN, DQ = (bench.KERNEL_NAMES[k] for k in ("fwd", "bwd_main", "bwd_dq"))
-CAUSAL_FWD = "fwd_kernel<64, 64, 32, 3>"
+CAUSAL_FWD = bench.CAUSAL_FWD_NAME
 D32_FWD = "fwd_kernel<32, 128, 64, 3>"
 
 
-def write_trace(path, w, k):
-    """The dispatch sequence of `bench.py --warmup w --steps k` with distinct durations per
-    window: idle steps (fwd 60, main 160), config 3 (other forward), the headline's timed steps
-    (fwd 54, main 136), forwards (53), kernel-level steps (fwd 52, main 135, dq 4), backwards
-    (main 137), then config 2 at d 32."""
+def write_trace(path, w, k, cfg=2):
+    """The dispatch sequence of `bench.py --warmup w --steps k` (config `cfg` as the headline)
+    with distinct durations per window: idle steps (fwd 60, main 160), another config (another
+    forward), the headline's timed steps (fwd 54, main 136), forwards (53), kernel-level steps
+    (fwd 52, main 135, dq 4), backwards (main 137), then config 2 at d 32."""
     b, h, s = bench.CONFIGS[2][2], bench.CONFIGS[2][3], bench.CONFIGS[2][4]
     grid = ((s + 127) // 128) * b * h
+    head, other = (FWD, grid), (CAUSAL_FWD, ((s + 63) // 64) * b * h)
+    if cfg == 3:  # config 3 as the headline (bench.py --causal); config 2 is then the other
+        head, other = other, head
+    FWD_, grid = head
     seq = []
-    seq += [(FWD, grid, 60.0), (MAIN, 1536, 160.0)] * (w + k)          # from idle
-    seq += [(CAUSAL_FWD, 1536, 40.0), (MAIN, 1536, 95.0)] * 30          # config 3
-    seq += [(FWD, grid, 70.0), (MAIN, 1536, 170.0)] * w                 # warm-up
-    seq += [(FWD, grid, 54.0), (MAIN, 1536, 136.0)] * k                 # timed
-    seq += [(FWD, grid, 53.0)] * k                                      # forwards
-    seq += [(FWD, grid, 52.0), (MAIN, 1536, 135.0), (DQ, 256, 4.0)] * k  # kernel-level
+    seq += [(FWD_, grid, 60.0), (MAIN, 1536, 160.0)] * (w + k)          # from idle
+    seq += [(other[0], other[1], 40.0), (MAIN, 1536, 95.0)] * 30        # another config
+    seq += [(FWD_, grid, 70.0), (MAIN, 1536, 170.0)] * w                 # warm-up
+    seq += [(FWD_, grid, 54.0), (MAIN, 1536, 136.0)] * k                 # timed
+    seq += [(FWD_, grid, 53.0)] * k                                      # forwards
+    seq += [(FWD_, grid, 52.0), (MAIN, 1536, 135.0), (DQ, 256, 4.0)] * k  # kernel-level
     seq += [(MAIN, 1536, 137.0)] * k                                    # backwards
     seq += [(D32_FWD, grid, 30.0), (MAIN, 1536, 80.0)] * 30             # d 32
     t = 1_000_000
@@ -58,20 +63,23 @@ def tables(text):
     return out
 
 
-def test_trace_windows(tmp_path):
+@pytest.mark.parametrize("cfg", [2, 3])
+def test_trace_windows(tmp_path, cfg):
     w, k = 5, 20
     trace = tmp_path / "kernel_trace.csv"
-    write_trace(trace, w, k)
+    write_trace(trace, w, k, cfg)
+    fwd = CAUSAL_FWD if cfg == 3 else FWD
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--trace-from", str(trace),
-                        "--warmup", str(w), "--steps", str(k)],
+                        "--warmup", str(w), "--steps", str(k)]
+                       + (["--causal"] if cfg == 3 else []),
                        capture_output=True, text=True, check=True)
     t = tables(r.stdout)
     by = {title.split(" (")[0]: rows for title, rows in t.items()}
-    assert by[f"The {k} timed forward+backward steps"] == {MAIN: (k, 136.0), FWD: (k, 54.0)}
-    assert by[f"The {k} op-level forwards"] == {FWD: (k, 53.0)}
+    assert by[f"The {k} timed forward+backward steps"] == {MAIN: (k, 136.0), fwd: (k, 54.0)}
+    assert by[f"The {k} op-level forwards"] == {fwd: (k, 53.0)}
     assert by[f"The {k} op-level backwards"] == {MAIN: (k, 137.0)}
-    assert by[f"The {k} kernel-level steps"] == {MAIN: (k, 135.0), FWD: (k, 52.0), DQ: (k, 4.0)}
-    assert by[f"The first {k} steps from idle"] == {MAIN: (k, 160.0), FWD: (k, 60.0)}
+    assert by[f"The {k} kernel-level steps"] == {MAIN: (k, 135.0), fwd: (k, 52.0), DQ: (k, 4.0)}
+    assert by[f"The first {k} steps from idle"] == {MAIN: (k, 160.0), fwd: (k, 60.0)}
 
 
 def write_counters(path, counter, rows):
