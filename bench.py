@@ -442,7 +442,8 @@ def main() -> int:
                     help="write profiles/traffic.json from two counter files and exit (no GPU)")
     ap.add_argument("--trace-from", metavar="KERNEL_TRACE_CSV",
                     help="print per-kernel durations of the headline's steps from a rocprofv3 "
-                         "kernel trace of this command with the same --warmup / --steps, and "
+                         "kernel trace of this command with the same --warmup / --steps (and "
+                         "--causal), and "
                          "exit (no GPU)")
     args = ap.parse_args()
     if args.traffic_from:
