@@ -419,6 +419,28 @@ def time_extra(torch, w: Workload, steps: int, warmup: int) -> dict:
     }
 
 
+STEP_BENCH = REPO / "candle-fused-attn_amd" / "lib" / "cfa_step_bench"
+
+
+def time_cxx_layer(b: int, h: int, s: int, d: int, causal: bool, warmup: int,
+                   steps: int) -> dict | None:
+    """Forward + backward steps through the C++ op layer (libcandle_fused_attn.so), timed by its
+    own program in a child process (lib/cfa_step_bench: fused_attention_qkv and the node's bwd per
+    step, outputs from the layer's memory pool, the node's kept workspace); None if it is not
+    built or fails."""
+    import subprocess
+    if not STEP_BENCH.exists():
+        log(f"bench: {STEP_BENCH} is not built: no C++ op layer step")
+        return None
+    cmd = [str(STEP_BENCH), str(b), str(h), str(s), str(d), str(int(causal)), str(warmup),
+           str(steps)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    if res.returncode != 0:
+        log(f"bench: C++ op layer step failed ({res.returncode}): {res.stderr.strip()[-400:]}")
+        return None
+    return json.loads(res.stdout.strip().splitlines()[-1])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -559,6 +581,17 @@ def main() -> int:
             del xw
         torch.cuda.synchronize()
 
+    cxx = None
+    if not args.no_extra:
+        # The same step through the C++ op layer, in a child process once this one is idle: its
+        # warm-up (at least 500 steps, about 0.1 s) brings the clocks back up after the child's
+        # start-up.
+        torch.cuda.synchronize()
+        cxx = time_cxx_layer(B, H, S, D, causal, max(args.warmup, 500), K)
+        if cxx:
+            log(f"bench: C++ op layer step {cxx['fwd_bwd_ms']:.4f} ms "
+                f"({cxx['fwd_bwd_ms'] / fwd_bwd_ms:.3f} x the C-ABI step)")
+
     f_fwd, f_bwd = w.flops()
     fwd_tflops = f_fwd / (fwd_ms * 1e-3) / 1e12
     total_tflops = (f_fwd + f_bwd) / (fwd_bwd_ms * 1e-3) / 1e12
@@ -604,7 +637,8 @@ def main() -> int:
                      + ("configs 3-5 timed (configs), " if extra else "")
                      + "W warm-up + K timed steps (value), K forwards, K kernel-level steps, "
                      + "K backwards"
-                     + (", config 2 at d 32 / 128 timed (configs)" if extra else "")),
+                     + (", config 2 at d 32 / 128 timed (configs), the C++ op layer's step "
+                        "(cxx_op_layer)" if extra else "")),
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_bwd_tflops": round(total_tflops, 3),
         "frac_fp32_peak": round(total_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
@@ -637,6 +671,16 @@ def main() -> int:
 
     if extra:
         result["configs"] = extra
+    if cxx:
+        result["cxx_op_layer"] = {
+            "fwd_bwd_ms": round(cxx["fwd_bwd_ms"], 5),
+            "vs_c_abi_step": round(cxx["fwd_bwd_ms"] / fwd_bwd_ms, 4),
+            "steps": cxx["steps"], "warmup": cxx["warmup"],
+            "how": ("candle_fused_attn::fused_attention_qkv + node->bwd per step "
+                    "(libcandle_fused_attn.so; outputs from its memory pool, the node's kept "
+                    "workspace), HIP events around K steps, in a child process "
+                    "(lib/cfa_step_bench) after the C-ABI legs"),
+        }
 
     if not args.no_accuracy:
         from oracle import oracle as orc

@@ -84,6 +84,23 @@ def build_host(verbose: bool = False) -> Path:
     return _run(host_command(tmp), tmp, HOST_LIB, verbose)
 
 
+STEP_BENCH_SRC = HOST / "step_bench.cpp"
+STEP_BENCH = LIB_DIR / "cfa_step_bench"
+
+
+def step_bench_command(out: Path = STEP_BENCH) -> list[str]:
+    return [hipcc(), "-O2", "-std=c++17", "-Wall", f"-I{HOST}", str(STEP_BENCH_SRC),
+            f"-L{LIB_DIR}", "-lcandle_fused_attn", "-lfattn", "-Wl,-rpath,$ORIGIN",
+            "-o", str(out)]
+
+
+def build_step_bench(verbose: bool = False) -> Path:
+    """Compile lib/cfa_step_bench (times steps through the C++ op layer; needs
+    libcandle_fused_attn.so built first)."""
+    tmp = STEP_BENCH.with_name(STEP_BENCH.name + ".tmp")
+    return _run(step_bench_command(tmp), tmp, STEP_BENCH, verbose)
+
+
 def host_test_command(out: Path = HOST_TEST) -> list[str]:
     rpath = "$ORIGIN/../../candle-fused-attn_amd/lib:$ORIGIN/../../oracle"
     return [hipcc(), "-O2", "-std=c++17", "-Wall", f"-I{HOST}", str(HOST_TEST_SRC),
@@ -100,3 +117,4 @@ def build_host_test(verbose: bool = False) -> Path:
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
     print(build_host(verbose="-v" in sys.argv))
+    print(build_step_bench(verbose="-v" in sys.argv))

@@ -254,7 +254,12 @@ def qkv_projection_of(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
     feeds fused_attention, tests/parity.rs:38-50), or None. Only where the op on the projection
     is the same computation with the same gradients: a head_dim the kernels take, rows
     float4-aligned, and q, k, v differentiable views of it (not detached leaves, none retaining
-    its own gradient), so every gradient reaches the projection either way."""
+    its own gradient, none with a backward hook registered), so every gradient reaches the
+    projection either way.
+
+    Routed, the graph runs from the output to the projection's node directly: the views' own
+    nodes are not on it, so torch.autograd.grad(out, [q, k, v]) finds them unused (take the
+    gradient of the projection, or turn routing off with set_projection_route(False))."""
     base = q._base
     if base is None or k._base is not base or v._base is not base or base.dim() != 3:
         return None
@@ -272,6 +277,8 @@ def qkv_projection_of(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
         if t.requires_grad != base.requires_grad or t.retains_grad:
             return None
         if t.requires_grad and t.grad_fn is None:
+            return None
+        if t._backward_hooks:  # a hook on the view would never run on the projection's path
             return None
     return base
 

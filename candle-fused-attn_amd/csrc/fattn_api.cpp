@@ -12,6 +12,8 @@
 #include <climits>
 #include <random>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -50,8 +52,8 @@ int64_t split_slots(int keys, int64_t d) {
 // The (b, h) pairs per chunk of the split dQ sum that a workspace of ws_bytes holds: b h when it
 // holds the whole split; else, at d <= 64, from the most pairs whose split partials, arrival
 // slots and done flags fit:
-//   causal: equal chunks, a multiple of 8 from 8 on (then a chunk's key blocks of one (b, h) share
-//     an XCD, as its own sums need);
+//   causal: equal chunks (the key blocks' own sums read the partials at device scope, so the
+//     XCDs a chunk's key blocks run on do not matter);
 //   non-causal: the most pairs whose key blocks fill whole rounds of the chip's workgroup slots
 //     (every key block walks all query tiles, so a partial round idles slots; the last chunk
 //     takes the rest);
@@ -78,14 +80,10 @@ int64_t split_chunk(int64_t b, int64_t h, int64_t s, int64_t d, size_t ws_bytes,
     if (lo >= quantum) lo -= lo % quantum;
     return lo == 0 || lo < min_pairs ? 0 : lo;
   }
-  const bool round8 = lo >= 8;
-  if (round8) lo &= ~int64_t{7};
   if (lo == 0 || lo < min_pairs) return 0;
-  // Equal chunks: ceil(total / chunks) <= lo, and a multiple of 8 up to lo stays <= lo.
+  // Equal chunks: ceil(total / chunks) <= lo.
   const int64_t chunks = (total + lo - 1) / lo;
-  int64_t c = (total + chunks - 1) / chunks;
-  if (round8) c = (c + 7) & ~int64_t{7};
-  return c;
+  return (total + chunks - 1) / chunks;
 }
 
 // The fewest (b, h) pairs a chunk should hold. A chunk is one launch of step 2: with too few key
@@ -103,13 +101,15 @@ int64_t min_chunk_pairs(int64_t b, int64_t h, int64_t s, int64_t d, bool causal)
 }
 
 // The workspace the library asks for within `limit` bytes: the whole split, else the split of the
-// largest chunk that is worth it (non-causal measure: the size takes no mask), else the turn
+// larger of the chunks each mask's rule takes (the size takes no mask; a run applies its own rule
+// to the workspace it is given, and each rule's chunk fits in the larger one), else the turn
 // hand-over's minimum (possibly over the limit: the caller decides).
 size_t workspace_within(int64_t b, int64_t h, int64_t s, int64_t d, size_t limit) {
   const Workspace l = workspace_layout(b, h, s, d);
   if (l.bytes_split <= limit) return l.bytes_split;
-  // (sized with the causal rule, whose chunk sizes the non-causal rule's fit too)
-  const int64_t c = split_chunk(b, h, s, d, limit, min_chunk_pairs(b, h, s, d, false), true);
+  const int64_t c = std::max(
+      split_chunk(b, h, s, d, limit, min_chunk_pairs(b, h, s, d, false), false),
+      split_chunk(b, h, s, d, limit, min_chunk_pairs(b, h, s, d, true), true));
   return c > 0 ? workspace_layout(1, c, s, d).bytes_split : l.bytes_min;
 }
 
@@ -138,6 +138,19 @@ unsigned long long next_epoch() {
 int fail(int code, const std::string& msg) {
   g_error = msg;
   return code;
+}
+
+// Whether the test hooks may act in this process: FATTN_TEST_HOOKS=1 in the environment when the
+// library was loaded (read once, by the library's static initialisation).
+const bool g_test_hooks = [] {
+  const char* v = std::getenv("FATTN_TEST_HOOKS");
+  return v != nullptr && std::strcmp(v, "1") == 0;
+}();
+
+int hooks_refused(const char* name) {
+  return fail(FATTN_EINVAL, std::string("fused_attention: ") + name +
+                                " is a test hook; it acts only when FATTN_TEST_HOOKS=1 was set "
+                                "before the library loaded");
 }
 
 int ok() {
@@ -845,15 +858,44 @@ int fattn_internal_sum_audit(int64_t b, int64_t h, int64_t s, int64_t d, int cau
   return 0;
 }
 
+// The test hooks below change how every later backward of the process runs. They act only in a
+// process that opted in before the library loaded (FATTN_TEST_HOOKS=1 in its environment, read
+// once, at load); otherwise they change nothing and return FATTN_EINVAL.
+
 // Test hook (not declared in include/fattn.h): step 2's dQ sums on (1, the default) or off (0:
 // step 3 sums every tile) for every later backward of the process. Returns the previous setting.
-int fattn_internal_step2_sums(int on) { return fattn::set_step2_sums(on != 0) ? 1 : 0; }
+int fattn_internal_step2_sums(int on) {
+  if (!g_test_hooks) return hooks_refused("fattn_internal_step2_sums");
+  return fattn::set_step2_sums(on != 0) ? 1 : 0;
+}
 
 // Test hook (not declared in include/fattn.h): step 2's non-causal summing workgroups of XCD x
 // sum the (b, h)s whose key blocks ran on XCD x + shift (mod 8) in every later backward of the
 // process (0, the default: their own XCD's), so that a test can make every sum read partials
 // written on another XCD. Returns the previous shift.
-int fattn_internal_sum_shift(int shift) { return fattn::set_sum_shift(shift); }
+int fattn_internal_sum_shift(int shift) {
+  if (!g_test_hooks) return hooks_refused("fattn_internal_sum_shift");
+  return fattn::set_sum_shift(shift);
+}
+
+// Test hook (not declared in include/fattn.h): the dQ sums of (b, h) pair `bh` (index b * h_count
+// + h; -1, the default: none) give up before their first poll in every later backward of the
+// process, as a wait that timed out would: where no step 3 follows they raise the guard word (3)
+// and write NaN into that pair's dQ rows; where step 3 follows it sums them. Returns the previous
+// pair.
+int fattn_internal_sum_give_up(int bh) {
+  if (!g_test_hooks) return hooks_refused("fattn_internal_sum_give_up");
+  return fattn::set_give_up_bh(bh);
+}
+
+// Test hook (not declared in include/fattn.h; read-only, always allowed): the hooks' current
+// settings, out[0] step 2's sums on, out[1] the sum shift, out[2] the give-up pair; returns 1 if
+// the hooks may act in this process, else 0.
+int fattn_internal_hooks(int64_t out[3]) {
+  if (!out) return FATTN_EINVAL;
+  fattn::test_hook_state(out);
+  return g_test_hooks ? 1 : 0;
+}
 
 int fattn_bwd_status(const void* workspace, size_t workspace_bytes, int64_t b, int64_t h,
                      int64_t s, void* stream, int* status) {

@@ -151,13 +151,19 @@ int bwd_split_keys(int64_t b, int64_t h, int64_t s, int d, int causal);
 bool bwd_step2_sums(int64_t b, int64_t h, int64_t s, int d, int causal);
 // Workgroups appended to step 2's grid for the non-causal sums (0 when causal or without sums).
 int64_t bwd_sum_blocks(int64_t b, int64_t h, int64_t s, int d, int causal);
-// Step 2's sums on (the default) or off for every later backward of the process, so that a test
-// can compare both; returns the previous setting.
+// Test hooks (the C ABI lets a process use them only when it opted in at load). Step 2's sums on
+// (the default) or off for every later backward of the process, so that a test can compare both;
+// returns the previous setting.
 bool set_step2_sums(bool on);
-// Test hook: the non-causal summing workgroups of XCD x sum the (b, h)s of XCD x + shift (mod 8)
-// in every later launch, so that their partials come from another XCD; returns the previous
-// shift.
+// The non-causal summing workgroups of XCD x sum the (b, h)s of XCD x + shift (mod 8) in every
+// later launch, so that their partials come from another XCD; returns the previous shift.
 int set_sum_shift(int shift);
+// Step 2's dQ sums of (b, h) pair `bh` (of the whole backward; -1: none, the default) give up
+// before their first poll in every later launch, as a wait that timed out would; returns the
+// previous pair.
+int set_give_up_bh(int bh);
+// The three hooks' current settings: step 2's sums on, the sum shift, the give-up pair.
+void test_hook_state(int64_t out[3]);
 // Step 3's grid: one workgroup per query tile, or (with step 2's sums) at most 256 workgroups
 // that each check a range of tiles and sum those not done.
 int64_t bwd_dq_grid(int64_t b, int64_t h, int64_t s, int d, int causal);

@@ -769,6 +769,9 @@ struct BwdArgs {
   // Test hook (0 in use): the non-causal summing workgroups of XCD x take the (b, h)s of XCD
   // x + sum_shift, so that every sum reads partials written on another XCD.
   int sum_shift;
+  // Test hook (-1 in use): the dQ sums of this (b, h) (its index in the whole backward) give up
+  // before their first poll, as a wait that timed out would.
+  int give_up_bh;
 };
 
 // Staggered walks make a key block wait on blocks of its own (b, h) that hold later tickets; that
@@ -1375,7 +1378,7 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
   const int need = a.causal ? min(nkb - 1, min(a.S - 1, j1 * kQT - 1) / a.kkeys) + 1 : nkb;
   if (tid < 64) {
     const unsigned long long* slots = a.arrive + static_cast<int64_t>(bh) * nkb;
-    const int polls = a.sums_final ? kSumPollsFinal : kSumPolls;
+    const int polls = a.bh0 + bh == a.give_up_bh ? 0 : a.sums_final ? kSumPollsFinal : kSumPolls;
     bool all = false;
     for (int it = 0; it < polls; ++it) {
       bool arrived = true;
@@ -1524,8 +1527,10 @@ __attribute__((amdgpu_waves_per_eu(KG == 1 || D == 32 ? BWD_WAVES : 2))) bwd_spl
   const int dt = w % kDT;
   auto dq_on = [&](int jt) { return kDqGroups == 1 || w / kDT == (jt + id) % kDqGroups; };
   // No turn waits here: the guard word reads 0 (unless a final sum's wait gave up; written
-  // through, as that raise is, so that no copy of it lingers in this XCD's L2).
-  if (id == 0 && tid == 0) {
+  // through, as that raise is, so that no copy of it lingers in this XCD's L2). Cleared by the
+  // backward's first launch only: a backward split into chunks of (b, h) launches step 2 once per
+  // chunk, and a later chunk must not clear what a sum of an earlier one raised.
+  if (id == 0 && tid == 0 && a.bh0 == 0) {
     __hip_atomic_store(a.ctrl + kCtrlGuard, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
@@ -1992,9 +1997,16 @@ bool bwd_needs_prep(bool split, int d) { return !split || d > 64; }
 namespace {
 std::atomic<int> g_step2_sums{1};
 std::atomic<int> g_sum_shift{0};
+std::atomic<int> g_give_up_bh{-1};
 }  // namespace
 bool set_step2_sums(bool on) { return g_step2_sums.exchange(on ? 1 : 0) != 0; }
 int set_sum_shift(int shift) { return g_sum_shift.exchange(shift & 7); }
+int set_give_up_bh(int bh) { return g_give_up_bh.exchange(bh < 0 ? -1 : bh); }
+void test_hook_state(int64_t out[3]) {
+  out[0] = g_step2_sums.load(std::memory_order_relaxed);
+  out[1] = g_sum_shift.load(std::memory_order_relaxed);
+  out[2] = g_give_up_bh.load(std::memory_order_relaxed);
+}
 
 int bwd_split_keys(int64_t b, int64_t h, int64_t s, int d, int causal) {
   // 128-key blocks (two 16-key groups per wave): half the dQ partials and half the per-tile
@@ -2097,7 +2109,8 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
   BwdArgs a{q,    k,     v,    d_o,  o,    lse,   dsum,       dqkv,  part,
             arrive, done, epoch_slot, epoch, static_cast<int>(nmain), plan, turn, ctrl, b, h, s,
             nkb,  ntile, scale, causal, stagger, kkeys, bh0, nbh,
-            arrive != nullptr && sums_final ? 1 : 0, g_sum_shift.load(std::memory_order_relaxed)};
+            arrive != nullptr && sums_final ? 1 : 0, g_sum_shift.load(std::memory_order_relaxed),
+            g_give_up_bh.load(std::memory_order_relaxed)};
   void* args[] = {&a};
   if (split && d <= 64) {
     const void* fn = d == 32 ? (kkeys == kBwdKeys

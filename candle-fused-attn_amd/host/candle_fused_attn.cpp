@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <functional>
 #include <numeric>
+#include <utility>
 
 #include "fattn.h"
 
@@ -135,24 +136,73 @@ Tensor saved(std::mutex& mu, const std::optional<Tensor>& slot) {
   return *slot;
 }
 
-// The backward workspace: fattn_bwd_workspace_bytes, taken on the stream and given back after
-// the launches that use it (stream order keeps it alive until they ran).
-std::shared_ptr<Storage> workspace(std::size_t b, std::size_t h, std::size_t s, std::size_t d,
-                                   hipStream_t stream, std::size_t* bytes) {
-  *bytes = fattn_bwd_workspace_bytes(static_cast<int64_t>(b), static_cast<int64_t>(h),
-                                     static_cast<int64_t>(s), static_cast<int64_t>(d));
-  return std::make_shared<Storage>(std::max<std::size_t>(*bytes, 256) / sizeof(float) + 1,
-                                   stream);
+// The layer's memory pool on the device that runs `stream` (the null stream: the current
+// device), made on first use: a stream-ordered pool whose release threshold is the maximum, so
+// memory given back stays in the pool for later allocations.
+hipMemPool_t device_pool(hipStream_t stream) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static hipMemPool_t pools[kMaxDevices] = {};
+  int dev = 0;
+  check_hip(stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev), "device of stream");
+  if (dev < 0 || dev >= kMaxDevices) fail("fused_attention: device index out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (pools[dev] == nullptr) {
+    hipMemPoolProps props{};
+    props.allocType = hipMemAllocationTypePinned;
+    props.handleTypes = hipMemHandleTypeNone;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t pool = nullptr;
+    check_hip(hipMemPoolCreate(&pool, &props), "memory pool");
+    uint64_t keep = UINT64_MAX;
+    check_hip(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep),
+              "memory pool threshold");
+    pools[dev] = pool;
+  }
+  return pools[dev];
 }
 
 }  // namespace
+
+// --- the kept backward workspace -----------------------------------------------------------------
+
+WorkspaceCache::Lease WorkspaceCache::take(std::size_t b, std::size_t h, std::size_t s,
+                                           std::size_t d, hipStream_t stream) {
+  const std::size_t bytes = fattn_bwd_workspace_bytes(
+      static_cast<int64_t>(b), static_cast<int64_t>(h), static_cast<int64_t>(s),
+      static_cast<int64_t>(d));
+  Lease kept;
+  {
+    std::lock_guard<std::mutex> lock(mu_);
+    std::swap(kept, kept_);
+  }
+  if (kept.ws && kept.stream == stream && kept.bytes >= bytes) {
+    kept.bytes = bytes;  // the size this backward asks for (its chunks follow from it)
+    return kept;
+  }
+  Lease fresh;
+  fresh.ws = std::make_shared<Storage>(std::max<std::size_t>(bytes, 256) / sizeof(float) + 1,
+                                       stream);
+  fresh.bytes = bytes;
+  fresh.stream = stream;
+  return fresh;
+}
+
+void WorkspaceCache::give_back(Lease lease) {
+  if (!lease.ws) return;
+  lease.bytes = lease.ws->size() * sizeof(float);
+  std::lock_guard<std::mutex> lock(mu_);
+  if (!kept_.ws || kept_.bytes < lease.bytes) std::swap(kept_, lease);
+}
 
 // --- Storage, Layout, Tensor -------------------------------------------------------------------
 
 Storage::Storage(std::size_t n, hipStream_t stream) : n_(n), stream_(stream), owned_(true) {
   if (n > 0) {
     void* p = nullptr;
-    check_hip(hipMallocAsync(&p, n * sizeof(float), stream), "allocation");
+    check_hip(hipMallocFromPoolAsync(&p, n * sizeof(float), device_pool(stream), stream),
+              "allocation");
     p_ = static_cast<float*>(p);
   }
 }
@@ -293,8 +343,7 @@ Tensor FusedAttentionQkv::bwd(const Tensor& qkv, const Tensor& res, const Tensor
     fail("fused_attention_qkv: O and L do not match the projection's shape");
   }
   Tensor dqkv = Tensor::empty({b, s, three_hd}, stream);
-  std::size_t ws_bytes = 0;
-  const auto ws = workspace(b, heads_, s, d, stream, &ws_bytes);
+  WorkspaceCache::Lease ws = ws_.take(b, heads_, s, d, stream);
   const auto shape = i64(ql.shape), strides = i64(ql.stride);
   const auto gshape = i64(grad.dims()), gstrides = i64(grad.stride());
   check_abi(fattn_qkv_backward(
@@ -302,7 +351,8 @@ Tensor FusedAttentionQkv::bwd(const Tensor& qkv, const Tensor& res, const Tensor
       static_cast<int64_t>(heads_), scale_, causal_ ? 1 : 0,
       res.storage_ptr() + res.layout().start_offset, l.storage_ptr() + l.layout().start_offset,
       grad.storage_ptr(), static_cast<int64_t>(grad.layout().start_offset), gshape.data(),
-      gstrides.data(), dqkv.storage_ptr(), ws->data(), ws_bytes, stream));
+      gstrides.data(), dqkv.storage_ptr(), ws.ws->data(), ws.bytes, stream));
+  ws_.give_back(std::move(ws));
   return dqkv;
 }
 
@@ -355,8 +405,7 @@ std::array<Tensor, 3> FusedAttention::bwd(const Tensor& q, const Tensor& k, cons
     fail("fused_attention: O and L do not match q's shape");
   }
   Tensor dqkv = Tensor::empty({b, s, 3, h, d}, stream);
-  std::size_t ws_bytes = 0;
-  const auto ws = workspace(b, h, s, d, stream, &ws_bytes);
+  WorkspaceCache::Lease ws = ws_.take(b, h, s, d, stream);
   std::vector<int64_t> sh[3], st[3];
   const Tensor* ops[3] = {&q, &k, &v};
   for (int i = 0; i < 3; ++i) {
@@ -371,7 +420,8 @@ std::array<Tensor, 3> FusedAttention::bwd(const Tensor& q, const Tensor& k, cons
       scale_, causal_ ? 1 : 0, res.storage_ptr() + res.layout().start_offset,
       l.storage_ptr() + l.layout().start_offset, grad.storage_ptr(),
       static_cast<int64_t>(grad.layout().start_offset), gshape.data(), gstrides.data(),
-      dqkv.storage_ptr(), ws->data(), ws_bytes, stream));
+      dqkv.storage_ptr(), ws.ws->data(), ws.bytes, stream));
+  ws_.give_back(std::move(ws));
   // dQ, dK, dV: narrow views of the one buffer, each [b, h, s, d] (src/lib.rs:484-485).
   auto part = [&](std::size_t i) { return dqkv.narrow(2, i, 1).squeeze(2).transpose(1, 2); };
   return {part(0), part(1), part(2)};

@@ -11,10 +11,14 @@
 // Layout: start offset, shape, strides, all in f32 elements), the op objects for the nodes candle
 // keeps in its autograd graph, and Error for candle_core::Error.
 //
-// Device memory of outputs, copies and the backward workspace is taken stream-ordered
-// (hipMallocAsync / hipFreeAsync on the caller's stream); every launch is asynchronous on that
-// stream, so that stream must outlive the tensors allocated on it (their storage is given back
-// on it). There is no CPU path: the operators run on the HIP device only.
+// Device memory of outputs, copies and the backward workspace is taken stream-ordered from a memory
+// pool this layer keeps per device (hipMallocFromPoolAsync / hipFreeAsync on the caller's stream):
+// the pool keeps what is given back for later allocations instead of returning it to the driver
+// (a caching allocator, as candle's and torch's are), so a steady-state step allocates nothing
+// from the driver; the memory is held until the process ends. Each op node also keeps its
+// backward workspace between backwards on one stream. Every launch is asynchronous on the
+// caller's stream, so that stream must outlive the tensors allocated on it (their storage is given
+// back on it). There is no CPU path: the operators run on the HIP device only.
 #ifndef CANDLE_FUSED_ATTN_HPP
 #define CANDLE_FUSED_ATTN_HPP
 
@@ -45,7 +49,7 @@ class Error : public std::runtime_error {
 // caller's (never freed).
 class Storage {
  public:
-  Storage(std::size_t n, hipStream_t stream);  // n floats, hipMallocAsync
+  Storage(std::size_t n, hipStream_t stream);  // n floats from the layer's pool, stream-ordered
   Storage(float* external, std::size_t n);     // wraps memory the caller owns
   ~Storage();
   Storage(const Storage&) = delete;
@@ -108,6 +112,29 @@ class Tensor {
 // multiples of 4 floats, d contiguous (src/lib.rs:163-168).
 bool float4_aligned(const Layout& l);
 
+// The backward workspace an op node keeps between backwards. The reference allocates its
+// temporaries per backward and drops them at return (src/cuda.rs:200-209); kept here, a
+// steady-state backward takes none. A backward takes the kept workspace out while it enqueues its
+// launches (a concurrent backward on the same node finds none and takes a new one, so no two
+// backwards share a workspace) and gives it back after; a backward on another stream, or needing
+// more bytes, takes a new one (the old one is freed stream-ordered on its own stream).
+class WorkspaceCache {
+ public:
+  struct Lease {
+    std::shared_ptr<Storage> ws;
+    std::size_t bytes = 0;
+    hipStream_t stream = nullptr;
+  };
+  // The workspace for a (b, h, s, d) backward on `stream` (fattn_bwd_workspace_bytes).
+  Lease take(std::size_t b, std::size_t h, std::size_t s, std::size_t d, hipStream_t stream);
+  // Keeps `lease` for the next backward (the larger one, if one was given back meanwhile).
+  void give_back(Lease lease);
+
+ private:
+  std::mutex mu_;
+  Lease kept_;
+};
+
 // The qkv-in, merged-out op (FusedAttentionQkv, src/lib.rs:493-590).
 class FusedAttentionQkv {
  public:
@@ -128,6 +155,7 @@ class FusedAttentionQkv {
   bool causal_;
   mutable std::mutex mu_;
   std::optional<Tensor> lse_;
+  WorkspaceCache ws_;
 };
 
 // The [b, h, s, d]-in, [b, s, h, d]-out op (FusedAttention, src/lib.rs:382-491).
@@ -148,6 +176,7 @@ class FusedAttention {
   bool causal_;
   mutable std::mutex mu_;
   std::optional<Tensor> lse_;
+  WorkspaceCache ws_;
 };
 
 // fused_attention_qkv (src/lib.rs:110-125): the output [b, s, h d] and the op node holding L

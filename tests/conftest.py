@@ -6,10 +6,15 @@ parity tests proper on an MI355X, through the C ABI.
 """
 from __future__ import annotations
 
+import os
 import sys
 from pathlib import Path
 
 import pytest
+
+# The library's test hooks (fattn_internal_*) act only in a process that sets this before the
+# library loads; the tests that compare step 2's dQ sums with step 3's use them.
+os.environ.setdefault("FATTN_TEST_HOOKS", "1")
 
 REPO = Path(__file__).resolve().parent.parent
 PKG = REPO / "candle-fused-attn_amd"

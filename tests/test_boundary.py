@@ -75,18 +75,22 @@ def test_workspace_size_is_aligned_and_monotone():
     assert L.fattn_bwd_workspace_split_bytes(1, 4, 16384, 64) > cap
     assert (L.fattn_bwd_workspace_bytes(1, 64, 16384, 64)
             == L.fattn_bwd_workspace_min_bytes(1, 64, 16384, 64))
-    # 256 MiB per pair: 15 fit, 8 (a multiple of 8) fill one round: chunks of 8
+    # The size takes no mask: the larger of the two rules' chunks. 256 MiB per pair, 15 fit:
+    # non-causal, 64 key blocks of 128 keys per pair, so multiples of 8 pairs fill whole rounds of
+    # the 512 slots: 8; causal, 15 pairs are under its minimum (four rounds of 768 slots in 64-key
+    # blocks: 24 pairs): none. Chunks of 8.
     assert (L.fattn_bwd_workspace_bytes(4, 16, 8192, 64)
             == L.fattn_bwd_workspace_split_bytes(1, 8, 8192, 64))
-    # 64 MiB per pair: 63 fit, rounded to 56 (8 | chunk), so 3 chunks, made equal: 48, 48, 32
+    # 64 MiB per pair, 63 fit: non-causal, 32 key blocks of 128 keys per pair, whole rounds of 512
+    # slots in multiples of 16 pairs: 48; causal, 3 equal chunks of 128 pairs: 43. So 48.
     assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 64)
             == L.fattn_bwd_workspace_split_bytes(1, 48, 4096, 64))
     assert L.fattn_bwd_workspace_split_bytes(1, 64, 4096, 64) > cap
-    # d 32, 32 MiB per pair: 127 fit, rounded to 120 (8 | chunk), so 2 chunks, made equal: 64, 64
-    # (each chunk's 64 x 32 key blocks of 128 keys fill the 768 workgroup slots several times)
+    # d 32, 32 MiB per pair, 127 fit: non-causal, 32 key blocks of 128 keys per pair, whole rounds
+    # of 768 slots in multiples of 24 pairs: 120; causal, 2 equal chunks: 64. So 120.
     assert L.fattn_bwd_workspace_split_bytes(8, 16, 4096, 32) > cap
     assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 32)
-            == L.fattn_bwd_workspace_split_bytes(1, 64, 4096, 32))
+            == L.fattn_bwd_workspace_split_bytes(1, 120, 4096, 32))
     assert (L.fattn_bwd_workspace_bytes(8, 16, 4096, 128)
             == L.fattn_bwd_workspace_min_bytes(8, 16, 4096, 128))
 
@@ -268,6 +272,10 @@ def test_projection_views_predicate():
     q3, k3, v3 = views(qkv)
     q3.retain_grad()                                      # a view that keeps its own gradient
     assert cfa.qkv_projection_of(q3, k3, v3) is None
+    for i in range(3):                                    # a backward hook on any one view
+        hooked = views(qkv)
+        hooked[i].register_hook(lambda g: g)
+        assert cfa.qkv_projection_of(*hooked) is None, f"hook on view {i}"
     wide = torch.zeros(b, s, 3 * h * d + 4)[..., : 3 * h * d]       # not a contiguous projection
     parts = [wide[..., i * h * d:(i + 1) * h * d].unflatten(-1, (h, d)).transpose(1, 2)
              for i in range(3)]
@@ -391,3 +399,61 @@ def test_step2_dq_sum_schedule(causal):
         # The benchmark's shapes: config 2 (s 240) keeps 64-key blocks, config 5 (s 1024) 128.
         assert sum_audit(64, 6, 240, 64, False)["keys"] == 64
         assert sum_audit(16, 16, 1024, 64, False)["keys"] == 128
+
+
+_HOOK_PROBE = r"""
+import ctypes, json, sys
+sys.path[:0] = [{repo!r}, {pkg!r}]
+from candle_fused_attn import _lib
+L = _lib.lib()
+for name in ("fattn_internal_step2_sums", "fattn_internal_sum_shift", "fattn_internal_sum_give_up"):
+    getattr(L, name).argtypes = [ctypes.c_int]
+    getattr(L, name).restype = ctypes.c_int
+L.fattn_internal_hooks.argtypes = [ctypes.POINTER(ctypes.c_int64)]
+L.fattn_internal_hooks.restype = ctypes.c_int
+audit = L.fattn_internal_sum_audit
+audit.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.POINTER(ctypes.c_int64)]
+audit.restype = ctypes.c_int
+def grid():
+    out = (ctypes.c_int64 * 6)()
+    assert audit(64, 6, 240, 64, 0, out) == 0
+    return out[0]
+rc = [L.fattn_internal_step2_sums(0), L.fattn_internal_sum_shift(3),
+      L.fattn_internal_sum_give_up(5)]
+err = _lib.last_error()
+state = (ctypes.c_int64 * 3)()
+allowed = L.fattn_internal_hooks(state)
+print(json.dumps(dict(rc=rc, err=err, allowed=allowed, state=list(state), grid=grid())))
+"""
+
+
+@pytest.mark.parametrize("opt_in", [False, True])
+def test_test_hooks_need_the_opt_in(opt_in):
+    """The test hooks change how every later backward of the process runs, so they act only in a
+    process that set FATTN_TEST_HOOKS=1 before the library loaded. Without it each refuses
+    (FATTN_EINVAL, a message naming the variable) and changes nothing: step 2's dQ-sum schedule at
+    config 2's shape keeps its appended summing workgroups, and the read-only state query shows the
+    defaults (sums on, shift 0, no give-up pair). With it the same calls act."""
+    import json
+    import os
+    import subprocess
+    import sys
+    env = {k: v for k, v in os.environ.items() if k != "FATTN_TEST_HOOKS"}
+    if opt_in:
+        env["FATTN_TEST_HOOKS"] = "1"
+    code = _HOOK_PROBE.format(repo=str(REPO), pkg=str(REPO / "candle-fused-attn_amd"))
+    res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=300)
+    assert res.returncode == 0, res.stderr
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    default_grid = sum_audit(64, 6, 240, 64, False)["grid"]
+    assert default_grid > 0
+    if opt_in:
+        assert r["rc"] == [1, 0, -1] and r["allowed"] == 1
+        assert r["state"] == [0, 3, 5]
+        assert r["grid"] == 0                     # sums off: nothing appended to step 2's grid
+    else:
+        assert r["rc"] == [_lib.FATTN_EINVAL] * 3 and r["allowed"] == 0
+        assert "FATTN_TEST_HOOKS" in r["err"]
+        assert r["state"] == [1, 0, -1]
+        assert r["grid"] == default_grid          # the schedule is unchanged

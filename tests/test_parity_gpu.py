@@ -688,9 +688,7 @@ def test_long_noncausal_128_key_blocks(orc, cuda):
     check_errors(orc, out, grad, ref_out, ref_grad, "b4 h32 s512")
     out2, grad2 = run("fused_qkv", qkv, g, h, 64, False, 0.125)
     assert torch.equal(bits(out2), bits(out)) and torch.equal(bits(grad2), bits(grad))
-    f = _lib.lib().fattn_internal_step2_sums
-    f.argtypes = [ctypes.c_int]
-    f.restype = ctypes.c_int
+    f = _hook("fattn_internal_step2_sums")
     prev = f(0)
     try:
         _, grad3 = run("fused_qkv", qkv, g, h, 64, False, 0.125)
@@ -783,6 +781,52 @@ def test_projection_views_take_the_qkv_node(orc, cuda, causal):
     assert not any(n == "_FusedAttentionBackward" for n in names), names
 
 
+def test_projection_views_hooks_and_autograd_grad(orc, cuda):
+    """Where routing the projection's views would skip what the caller attached to a view, it is
+    not routed: a backward hook on k makes fused_attention take the general node, the hook runs
+    and sees k's gradient, and the projection's gradient equals the routed one bit for bit. Routed,
+    the views are not on the graph (torch.autograd.grad(out, [q, k, v]) finds them unused, as
+    documented), while the projection's gradient is there; with routing off, autograd.grad on the
+    views returns the projection gradient's three parts bit for bit."""
+    b, h, s, d = 2, 3, 97, 64
+    x, dout, qkv, g = seeded_qkv(orc, b, h, s, 9, cuda)
+    want = run("fused_qkv", qkv, g, h, d, False, 0.125)[1].view(b, s, 3, h, d)
+    gout = g.view(b, s, h, d).transpose(1, 2)
+
+    seen = {}
+    xx = qkv.detach().clone().requires_grad_(True)
+    q, k, v = qkv_views(xx, h, d)
+    k.register_hook(lambda grad: seen.setdefault("k", grad.detach().clone()))
+    out = cfa.fused_attention(q, k, v, 0.125, False)
+    fn = out.grad_fn
+    while fn is not None and "FusedAttention" not in type(fn).__name__:
+        fn = fn.next_functions[0][0] if fn.next_functions else None
+    assert fn is not None and "Qkv" not in type(fn).__name__, "not the general node"
+    out.backward(gout)
+    assert "k" in seen, "the hook on k did not run"
+    assert torch.equal(bits(seen["k"]), bits(want[:, :, 1].transpose(1, 2))), "k's gradient"
+    assert torch.equal(bits(xx.grad.view(b, s, 3, h, d)), bits(want)), "projection gradient"
+
+    xx = qkv.detach().clone().requires_grad_(True)
+    q, k, v = qkv_views(xx, h, d)
+    out = cfa.fused_attention(q, k, v, 0.125, False)
+    with pytest.raises(RuntimeError):
+        torch.autograd.grad(out, [q, k, v], gout)
+    (gx,) = torch.autograd.grad(out, [xx], gout)
+    assert torch.equal(bits(gx.view(b, s, 3, h, d)), bits(want))
+
+    prev = cfa.set_projection_route(False)
+    try:
+        xx = qkv.detach().clone().requires_grad_(True)
+        q, k, v = qkv_views(xx, h, d)
+        out = cfa.fused_attention(q, k, v, 0.125, False)
+        grads = torch.autograd.grad(out, [q, k, v], gout)
+    finally:
+        cfa.set_projection_route(prev)
+    for i, gi in enumerate(grads):
+        assert torch.equal(bits(gi.contiguous()), bits(want[:, :, i].transpose(1, 2).contiguous()))
+
+
 def ws_layout(b, h, s, d):
     """Byte offsets of the backward workspace's parts (restated from fattn_api.cpp's
     workspace_layout; the library's reported sizes pin it)."""
@@ -835,10 +879,17 @@ def step2_summed_tiles(qkv, dout, h, d, causal, grad_want):
 
 
 def _hook(name):
+    """A test hook of libfattn.so; it refuses (FATTN_EINVAL) unless FATTN_TEST_HOOKS=1 was set
+    before the library loaded (tests/conftest.py sets it)."""
     f = getattr(_lib.lib(), name)
     f.argtypes = [ctypes.c_int]
     f.restype = ctypes.c_int
-    return f
+
+    def call(x):
+        rc = f(x)
+        assert rc != _lib.FATTN_EINVAL, _lib.last_error()
+        return rc
+    return call
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -1319,3 +1370,75 @@ def test_split_by_chunks_matches_whole(cuda, causal, d):
         small = L.fattn_bwd_workspace_split_bytes(1, 8, s, d)   # chunks of 8: turns instead
         say(f"workspace for 8 pairs ({small >> 20} MiB): the turn hand-over")
         assert torch.equal(bits(backward(small)), bits(whole))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sum_give_up_raises_guard_and_writes_nan(cuda, causal):
+    """A dQ sum in step 2 whose bounded wait gives up (forced from the host by a test hook: the
+    sums of one (b, h) pair give up before their first poll, so every kernel still ends normally)
+    leaves NaN in exactly that pair's dQ rows and raises the guard word to 3 where no step 3
+    follows: a whole launch, and a backward split into chunks of pairs with the pair in the
+    first chunk (the second chunk's launch must not clear what the first one raised). Every
+    other element is bit-identical to a run without the hook. With step 3 to follow (the kernel-level steps), step 3 sums that pair's tiles: the
+    gradient is the hookless one and the guard word reads 0."""
+    b, h, s, d = (2, 12, 4096, 64) if not causal else (6, 16, 4096, 64)
+    pairs = 16 if not causal else 48          # chunks: 16 + 8 non-causal, 48 + 48 causal
+    victim = 3                                # a pair of the first chunk
+    L = _lib.lib()
+    give_up = _hook("fattn_internal_sum_give_up")
+    g = torch.Generator(device=cuda).manual_seed(11)
+    qkv = torch.randn(b, s, 3 * h * d, generator=g, device=cuda)
+    dout = torch.randn(b, s, h * d, generator=g, device=cuda)
+    st = _lib.arr([s * 3 * h * d, d, 3 * h * d])
+    gst = _lib.arr([s * h * d, d, h * d])
+    qp, kp, vp = (ctypes.c_void_p(qkv.data_ptr() + i * h * d * 4) for i in range(3))
+    stream = _st(qkv)
+    o = torch.empty(b, s, h * d, device=cuda)
+    lse = torch.empty(b, h, s, device=cuda)
+    _lib.check(L.fattn_fwd_f32(qp, kp, vp, _p(o), _p(lse), b, h, s, d, 0.125, int(causal), st, st,
+                               st, stream))
+
+    def status_of(ws, n):
+        status = ctypes.c_int(-1)
+        _lib.check(L.fattn_bwd_status(_p(ws), n, b, h, s, stream, ctypes.byref(status)))
+        return status.value
+
+    def backward(n, kernel_level=False):
+        ws = torch.empty(n, dtype=torch.uint8, device=cuda)
+        out = torch.full_like(qkv, float("nan"))
+        if kernel_level:
+            _lib.check(L.fattn_bwd_main_f32(qp, kp, vp, _p(o), _p(dout), _p(lse), _p(out), _p(ws),
+                                            n, b, h, s, d, 0.125, int(causal), st, st, st, gst,
+                                            stream))
+            _lib.check(L.fattn_bwd_dq_f32(_p(out), _p(ws), n, b, h, s, d, 0.125, int(causal),
+                                          stream))
+        else:
+            _lib.check(L.fattn_bwd_f32(qp, kp, vp, _p(o), _p(dout), _p(lse), _p(out), _p(ws), n,
+                                       b, h, s, d, 0.125, int(causal), st, st, st, gst, stream))
+        return out, status_of(ws, n)
+
+    whole_n = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
+    chunk_n = L.fattn_bwd_workspace_split_bytes(1, pairs, s, d)
+    ref, st0 = backward(whole_n)
+    assert st0 == 0 and torch.isfinite(ref).all()
+    vb, vh = divmod(victim, h)
+    mask = torch.zeros(b, s, 3, h, d, dtype=torch.bool, device=cuda)
+    mask[vb, :, 0, vh] = True                 # the pair's dQ rows
+    mask = mask.view_as(ref)
+    prev = give_up(victim)
+    try:
+        for name, n, level in (("whole launch", whole_n, False), ("chunks", chunk_n, False),
+                               ("kernel-level steps", whole_n, True)):
+            say(f"give-up pair {victim} (b {vb}, h {vh}) causal={causal}: {name}")
+            got, status = backward(n, level)
+            if level:
+                assert status == 0, f"{name}: guard {status}"
+                assert torch.equal(bits(got), bits(ref)), f"{name}: step 3 did not sum the pair"
+                continue
+            assert status == 3, f"{name}: guard word {status}, expected 3"
+            assert torch.isnan(got[mask]).all(), f"{name}: the pair's dQ rows are not all NaN"
+            assert torch.equal(bits(got[~mask]), bits(ref[~mask])), f"{name}: other elements"
+    finally:
+        give_up(prev)
+    again, st1 = backward(chunk_n)            # the hook off again: the next backward is clean
+    assert st1 == 0 and torch.equal(bits(again), bits(ref))
