@@ -303,28 +303,19 @@ def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
     return 0
 
 
-def summarize_trace(trace_csv: str, warmup: int, steps: int, cfg: int = 2) -> int:
-    """Per-kernel durations of the headline's GPU work, from a rocprofv3 --kernel-trace file of
-    `bench.py --warmup W --steps K` (same W and K): the K timed forward+backward steps, the K
-    op-level forwards and backwards (`fwd_ms`, `bwd_ms`, which price `roofline`), the K
-    kernel-level steps (`kernels_us`), and the first K steps from idle. Configs 3-5 run the same
-    kernel names, so the dispatches are split into steps (a step starts at a forward launch, or at
-    a step-2 launch in a step that already holds one) and config 2's steps picked by the forward's
-    name and grid; the headline's are the run of them after configs 3-5, and its K backwards the
-    K steps after that run."""
-    rows = []
-    with open(trace_csv, newline="") as f:
-        for r in csv.DictReader(f):
-            if "fattn::" not in r["Kernel_Name"]:
-                continue
-            name = r["Kernel_Name"].split("fattn::(anonymous namespace)::", 1)[-1]
-            name = name.split("(", 1)[0].replace("void ", "")
-            wgs = int(r["Grid_Size_X"]) // max(int(r["Workgroup_Size_X"]), 1)
-            rows.append((int(r["Start_Timestamp"]), name, wgs,
-                         (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
-    rows.sort()
-    # The headline's forward: config 2's non-causal kernel (128-query blocks), or with --causal
-    # config 3's (64-query blocks).
+def _kernel_label(raw: str) -> str:
+    name = raw.split("fattn::(anonymous namespace)::", 1)[-1]
+    return name.split("(", 1)[0].replace("void ", "")
+
+
+def _headline_windows(rows: list, warmup: int, steps: int, cfg: int) -> dict | None:
+    """The headline's windows from a time-ordered list of (start, kernel, workgroups, payload)
+    dispatches of `bench.py --warmup W --steps K`: {"timed", "fwds", "kern", "bwds", "idle"}, each
+    a list of steps, a step a list of (kernel, workgroups, payload); None if the run holds no such
+    window. Configs 3-5 run the same kernel names, so the dispatches are split into steps (a step
+    starts at a forward launch, or at a step-2 launch in a step that already holds one) and the
+    main config's steps picked by the forward's name and grid; the headline's are the run of them
+    after configs 3-5, its K forwards, K kernel-level steps and K backwards the steps after it."""
     b, h, s = CONFIGS[cfg][2], CONFIGS[cfg][3], CONFIGS[cfg][4]
     qb = 64 if CONFIGS[cfg][5] else 128
     main_fwd = (CAUSAL_FWD_NAME if CONFIGS[cfg][5] else KERNEL_NAMES["fwd"],
@@ -334,15 +325,15 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int, cfg: int = 2) -> in
     def step2(name):
         return name.startswith(("bwd_split_kernel", "bwd_kernel"))
 
-    for t, name, wgs, us in rows:
+    for _, name, wgs, payload in rows:
         if (name.startswith("fwd_kernel") or not steps_seq
                 or (step2(name) and any(step2(n) for n, _, _ in steps_seq[-1]))):
             steps_seq.append([])
-        steps_seq[-1].append((name, wgs, us))
+        steps_seq[-1].append((name, wgs, payload))
     is_main = [st[0][0] == main_fwd[0] and st[0][1] == main_fwd[1] for st in steps_seq]
-    # Runs of consecutive config-2 steps: the idle run opens the trace (unless --no-extra, when
-    # the trace is one run); the headline's is the first run after another config's steps that
-    # holds the W warm-up, K timed, K forward and K kernel-level steps.
+    # Runs of consecutive main-config steps: the idle run opens the run (unless --no-extra, when
+    # it is one run); the headline's is the first run after another config's steps that holds the
+    # W warm-up, K timed, K forward and K kernel-level steps.
     runs, start = [], None
     for i, m in enumerate(is_main + [False]):
         if m and start is None:
@@ -358,13 +349,38 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int, cfg: int = 2) -> in
                 if runs and runs[0][0] == 0 and runs[0][1] >= warmup + steps else [])
         later = [r for r in runs if r[0] > 0 and r[1] - r[0] >= need]
         first = later[0][0] if later else len(steps_seq)
-    timed = steps_seq[first + warmup:first + warmup + steps]
-    fwds = steps_seq[first + warmup + steps:first + warmup + 2 * steps]
-    kern = steps_seq[first + warmup + 2 * steps:first + warmup + 3 * steps]
-    bwds = steps_seq[first + warmup + 3 * steps:first + warmup + 4 * steps]
-    if len(timed) < steps or len(kern) < steps:
-        print(f"bench.py: the trace holds no run of {need} config-{cfg} steps after the other "
-              "configs", file=sys.stderr)
+    win = {
+        "timed": steps_seq[first + warmup:first + warmup + steps],
+        "fwds": steps_seq[first + warmup + steps:first + warmup + 2 * steps],
+        "kern": steps_seq[first + warmup + 2 * steps:first + warmup + 3 * steps],
+        "bwds": steps_seq[first + warmup + 3 * steps:first + warmup + 4 * steps],
+        "idle": idle,
+    }
+    if len(win["timed"]) < steps or len(win["kern"]) < steps:
+        return None
+    if not (len(win["bwds"]) == steps and all(step2(st[0][0]) for st in win["bwds"])):
+        win["bwds"] = []
+    return win
+
+
+def summarize_trace(trace_csv: str, warmup: int, steps: int, cfg: int = 2) -> int:
+    """Per-kernel durations of the headline's GPU work, from a rocprofv3 --kernel-trace file of
+    `bench.py --warmup W --steps K` (same W and K): the K timed forward+backward steps, the K
+    op-level forwards and backwards (`fwd_ms`, `bwd_ms`, which price `roofline`), the K
+    kernel-level steps (`kernels_us`), and the first K steps from idle (_headline_windows)."""
+    rows = []
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            if "fattn::" not in r["Kernel_Name"]:
+                continue
+            wgs = int(r["Grid_Size_X"]) // max(int(r["Workgroup_Size_X"]), 1)
+            rows.append((int(r["Start_Timestamp"]), _kernel_label(r["Kernel_Name"]), wgs,
+                         (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    rows.sort()
+    win = _headline_windows(rows, warmup, steps, cfg)
+    if win is None:
+        print(f"bench.py: the trace holds no run of {warmup + 3 * steps} config-{cfg} steps after "
+              "the other configs", file=sys.stderr)
         return 1
 
     def table(title, seq):
@@ -380,14 +396,120 @@ def summarize_trace(trace_csv: str, warmup: int, steps: int, cfg: int = 2) -> in
             print(f"| `{name}` | {len(v)} | {statistics.mean(v):.1f} | {statistics.median(v):.1f} "
                   f"| {min(v):.1f} | {max(v):.1f} | {100 * sum(v) / total:.1f} % |")
 
-    table(f"The {steps} timed forward+backward steps (after {warmup} warm-up steps)", timed)
-    table(f"The {steps} op-level forwards (`fwd_ms`, `roofline.fwd_kernel_achieved`)", fwds)
-    if len(bwds) == steps and all(step2(st[0][0]) for st in bwds):
-        table(f"The {steps} op-level backwards (`bwd_ms`, `roofline.achieved`)", bwds)
-    table(f"The {steps} kernel-level steps (`kernels_us`)", kern)
-    if idle:
+    table(f"The {steps} timed forward+backward steps (after {warmup} warm-up steps)", win["timed"])
+    table(f"The {steps} op-level forwards (`fwd_ms`, `roofline.fwd_kernel_achieved`)", win["fwds"])
+    if win["bwds"]:
+        table(f"The {steps} op-level backwards (`bwd_ms`, `roofline.achieved`)", win["bwds"])
+    table(f"The {steps} kernel-level steps (`kernels_us`)", win["kern"])
+    if win["idle"]:
         table(f"The first {steps} steps from idle (after {warmup} warm-up steps; "
-              "`fwd_bwd_from_idle_ms`)", idle)
+              "`fwd_bwd_from_idle_ms`)", win["idle"])
+    return 0
+
+
+# Counters per dispatch that the summary derives figures from (any subset may be present).
+MFMA_CYCLES = 32            # v_mfma_f32_16x16x4_f32: 8 passes of 4 cycles on one SIMD
+N_SIMDS, N_CUS, N_XCDS = 1024, 256, 8
+
+
+def summarize_counters(csvs: list[str], warmup: int, steps: int, cfg: int = 2) -> int:
+    """SQ / GRBM counters of the headline's K timed steps, per kernel, from the
+    `counter_collection.csv` files of `rocprofv3 --pmc ... -- python3 bench.py --warmup W --steps K
+    ...` runs (one file per counter pass; the same W, K and main config): each pass's dispatches
+    are split into steps as _headline_windows does, the timed window's dispatches of each kernel
+    averaged, and the passes merged. GRBM_GUI_ACTIVE comes summed over the 8 XCDs (per dispatch it
+    reads 8 x the kernel's duration in GPU cycles), so the GPU-busy cycles of a dispatch are an
+    eighth of it. Derived (where the counters are there): MFMA busy = SIMD cycles with the matrix
+    core busy / (GPU-busy cycles x 1024 SIMDs); the MFMA instructions' own cycles (32 each)
+    against that; waves per SIMD = 4 SQ_WAVE_CYCLES (quad-cycles) / (GPU-busy cycles x 1024
+    SIMDs); non-MFMA VALU issue (4 cycles an instruction) as a share of SIMD cycles; per MFMA
+    instruction: other VALU, SALU, LDS, transcendental instructions; executed MFMA GFLOP (512 FLOP
+    per F32 MOPS unit); wave time waiting on a dependency (SQ_WAIT_ANY: memory, LDS, barrier),
+    waiting to issue (SQ_WAIT_INST_ANY: its pipe busy with other waves) and issuing
+    (SQ_ACTIVE_INST_ANY) as shares of the waves' cycles. Printed as a markdown table."""
+    per: dict[str, dict[str, list[float]]] = {}
+    calls: dict[str, int] = {}
+    for path in csvs:
+        disp: dict[int, dict] = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if "fattn::" not in r["Kernel_Name"]:
+                    continue
+                d = disp.setdefault(int(r["Dispatch_Id"]), {
+                    "t": int(r["Start_Timestamp"]), "name": _kernel_label(r["Kernel_Name"]),
+                    "wgs": int(r["Grid_Size"]) // max(int(r["Workgroup_Size"]), 1), "c": {}})
+                d["c"][r["Counter_Name"]] = d["c"].get(r["Counter_Name"], 0.0) + float(
+                    r["Counter_Value"])
+        rows = sorted((d["t"], d["name"], d["wgs"], d["c"]) for d in disp.values())
+        win = _headline_windows(rows, warmup, steps, cfg)
+        if win is None:
+            print(f"bench.py: {path} holds no run of {warmup + 3 * steps} config-{cfg} steps",
+                  file=sys.stderr)
+            return 1
+        seen: dict[str, int] = {}
+        for st in win["timed"]:
+            for name, _, c in st:
+                seen[name] = seen.get(name, 0) + 1
+                slot = per.setdefault(name, {})
+                for k, v in c.items():
+                    slot.setdefault(k, []).append(v)
+        for name, n in seen.items():
+            calls[name] = max(calls.get(name, 0), n)
+    mean = {n: {k: statistics.mean(v) for k, v in c.items()} for n, c in per.items()}
+
+    def derived(c: dict) -> dict:
+        out = {}
+        gui = c.get("GRBM_GUI_ACTIVE", 0.0) / N_XCDS
+        mfma = c.get("SQ_INSTS_MFMA")
+        if gui and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+            out["MFMA busy (% of SIMD cycles)"] = 100 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * N_SIMDS)
+        if mfma and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+            out["MFMA instruction cycles / MFMA busy cycles"] = (
+                mfma * MFMA_CYCLES / c["SQ_VALU_MFMA_BUSY_CYCLES"])
+        if gui and "SQ_WAVE_CYCLES" in c:
+            out["waves per SIMD (average)"] = 4 * c["SQ_WAVE_CYCLES"] / (gui * N_SIMDS)
+        if mfma and gui and "SQ_INSTS_VALU" in c:
+            out["non-MFMA VALU issue (% of SIMD cycles)"] = (
+                100 * 4 * (c["SQ_INSTS_VALU"] - mfma) / (gui * N_SIMDS))
+        if mfma:
+            if "SQ_INSTS_VALU" in c:
+                out["other VALU per MFMA"] = (c["SQ_INSTS_VALU"] - mfma) / mfma
+            for k, label in (("SQ_INSTS_SALU", "SALU per MFMA"), ("SQ_INSTS_LDS", "LDS per MFMA"),
+                             ("SQ_INSTS_VALU_TRANS_F32", "transcendental per MFMA"),
+                             ("SQ_INSTS_BRANCH", "branches per MFMA"),
+                             ("SQ_INSTS_SMEM", "scalar loads per MFMA"),
+                             ("SQ_INSTS_VMEM", "vector memory per MFMA")):
+                if k in c:
+                    out[label] = c[k] / mfma
+        if "SQ_INSTS_VALU_MFMA_MOPS_F32" in c:
+            out["MFMA GFLOP executed"] = c["SQ_INSTS_VALU_MFMA_MOPS_F32"] * 512 / 1e9
+        if c.get("SQ_WAVE_CYCLES"):
+            for k, label in (("SQ_WAIT_ANY", "wave cycles waiting (%)"),
+                             ("SQ_WAIT_INST_ANY", "wave cycles waiting to issue (%)"),
+                             ("SQ_ACTIVE_INST_ANY", "wave cycles issuing (%)")):
+                if k in c:
+                    out[label] = 100 * c[k] / c["SQ_WAVE_CYCLES"]
+        if gui:
+            out["GPU-busy cycles (GRBM_GUI_ACTIVE / 8)"] = gui
+        return out
+
+    names = sorted(mean, key=lambda n: -mean[n].get("GRBM_GUI_ACTIVE", 0.0))
+    der = {n: derived(mean[n]) for n in names}
+    print(f"\nThe {steps} timed steps after {warmup} warm-up steps (config {cfg}): mean per "
+          f"dispatch over {len(csvs)} counter run(s)\n")
+    print("| | " + " | ".join(f"`{n}`" for n in names) + " |")
+    print("|---|" + "--:|" * len(names))
+    print("| dispatches per run | " + " | ".join(str(calls[n]) for n in names) + " |")
+    keys = []
+    for n in names:
+        keys += [k for k in der[n] if k not in keys]
+    for k in keys:
+        print(f"| {k} | " + " | ".join(f"{der[n][k]:.4g}" if k in der[n] else "" for n in names)
+              + " |")
+    raw = sorted({k for n in names for k in mean[n]})
+    for k in raw:
+        print(f"| {k} | " + " | ".join(f"{mean[n][k]:.6g}" if k in mean[n] else "" for n in names)
+              + " |")
     return 0
 
 
@@ -462,6 +584,9 @@ def main() -> int:
                          "to scale rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/traffic.json from two counter files and exit (no GPU)")
+    ap.add_argument("--counters-from", nargs="+", metavar="COUNTER_CSV",
+                    help="no GPU: summarise rocprofv3 --pmc counter files of this command's "
+                         "timed steps (same --warmup, --steps, --causal)")
     ap.add_argument("--trace-from", metavar="KERNEL_TRACE_CSV",
                     help="print per-kernel durations of the headline's steps from a rocprofv3 "
                          "kernel trace of this command with the same --warmup / --steps (and "
@@ -470,6 +595,9 @@ def main() -> int:
     args = ap.parse_args()
     if args.traffic_from:
         return summarize_traffic(*args.traffic_from)
+    if args.counters_from:
+        return summarize_counters(args.counters_from, max(args.warmup, 1), max(args.steps, 1),
+                                  3 if args.causal else 2)
     if args.trace_from:
         return summarize_trace(args.trace_from, max(args.warmup, 1), max(args.steps, 1),
                                3 if args.causal else 2)

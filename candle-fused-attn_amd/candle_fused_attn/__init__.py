@@ -16,6 +16,7 @@ from .ops import (
     qkv_projection_of,
     reads_in_place,
     set_dq_sum,
+    set_projection_route,
 )
 
 __all__ = [
@@ -30,5 +31,6 @@ __all__ = [
     "qkv_projection_of",
     "reads_in_place",
     "set_dq_sum",
+    "set_projection_route",
     "version",
 ]

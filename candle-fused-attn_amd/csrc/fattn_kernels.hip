@@ -641,6 +641,7 @@ fwd_kernel(FwdArgs a) {
   }
 
   if (wave_live) {
+    float lrow[kFwdNT];  // L of this lane's row in each column tile
 #pragma unroll
     for (int n = 0; n < kFwdNT; ++n) {
       // The row sum: the four lanes of a query hold partial sums over disjoint keys; every lane
@@ -648,17 +649,35 @@ fwd_kernel(FwdArgs a) {
       const float l0 = __shfl(lsum[n], lo), l1 = __shfl(lsum[n], lo + 16);
       const float l2 = __shfl(lsum[n], lo + 32), l3 = __shfl(lsum[n], lo + 48);
       const float l = (l0 + l1) + (l2 + l3);
-      const int qi = qw0 + 16 * n + lo;
-      if (qi < S) {
-        const float inv = 1.0f / l;
-        float* orow = a.o + ((static_cast<int64_t>(b) * S + qi) * a.H + h) * D;
+      lrow[n] = m[n] * ascale + logf(l);
+      // O as whole 128-byte lines per store instruction (row-wise 64-byte pieces reached HBM
+      // unmerged: 33.5 MB written at b 64 h 6 s 240 for 24.0 MB of O and L; 24.0 MB this way).
+      // Lane (lo, g) holds dims 16 mt + 4 g .. + 3 of row lo; for each pair of dim tiles
+      // (2 p, 2 p + 1) lanes lo and lo ^ 8 swap a float4 (DPP row rotate by 8), so that the first
+      // store writes rows 0-7 and the second rows 8-15 of the column tile, each row's dims
+      // 32 p .. 32 p + 31 whole: lanes lo < 8 the first 16 of them, lanes lo >= 8 the second 16.
+      // Rows past S hold garbage and are not stored.
+      const float inv = 1.0f / l;
+      const bool hi = lo >= 8;
+      const int r1 = qw0 + 16 * n + (lo & 7), r2 = r1 + 8;
+      float* const o1 = a.o + ((static_cast<int64_t>(b) * S + r1) * a.H + h) * D;
+      float* const o2 = o1 + static_cast<int64_t>(8) * a.H * D;
 #pragma unroll
-        for (int mt = 0; mt < kDT; ++mt) st4_nt(orow + 16 * mt + 4 * g, acc[n][mt] * inv);
-        if (g == 0) {
-          __builtin_nontemporal_store(m[n] * ascale + logf(l),
-                                      a.lse + static_cast<int64_t>(bh) * S + qi);
-        }
+      for (int p = 0; p < kDT / 2; ++p) {
+        const f4 A = acc[n][2 * p] * inv, B = acc[n][2 * p + 1] * inv;
+        f4 R;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) R[e] = dpp<0x128>(hi ? A[e] : B[e]);
+        const int col = 32 * p + (hi ? 16 : 0) + 4 * g;
+        if (r1 < S) st4_nt(o1 + col, hi ? R : A);
+        if (r2 < S) st4_nt(o2 + col, hi ? B : R);
       }
+    }
+    // L of column tile g from lane group g: one store covers the wave's rows.
+    if (g < kFwdNT) {
+      const int qi = qw0 + 16 * g + lo;
+      const float lv = kFwdNT == 2 && g == 1 ? lrow[kFwdNT - 1] : lrow[0];
+      if (qi < S) __builtin_nontemporal_store(lv, a.lse + static_cast<int64_t>(bh) * S + qi);
     }
   }
 }
