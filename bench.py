@@ -264,10 +264,23 @@ def traffic_entry():
     return res
 
 
-def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
-    """profiles/traffic.json from two counter runs of `bench.py --calibrate-copy` (one counter
-    each): per kernel the mean FETCH_SIZE / WRITE_SIZE over its launches, in KiB, each scaled by
-    what the same counter reads for the 256 MiB device copy (bytes it is known to move)."""
+def traffic_path(cfg: int) -> Path:
+    """Where the traffic summary of a config's run goes: profiles/traffic.json for config 2 (the
+    headline's roofline.traffic), profiles/traffic_config<N>.json otherwise."""
+    return TRAFFIC if cfg == 2 else TRAFFIC.with_name(f"traffic_config{cfg}.json")
+
+
+# Kernel roles by name prefix (the traffic summary's keys).
+KERNEL_ROLES = (("fwd", "fwd_kernel"), ("bwd_prep", "prep_kernel"),
+                ("bwd_main", "bwd_split_kernel"), ("bwd_main", "bwd_kernel"),
+                ("bwd_dq", "dq_kernel"))
+
+
+def summarize_traffic(fetch_csv: str, write_csv: str, cfg: int = 2) -> int:
+    """profiles/traffic.json (config 2) or profiles/traffic_config<N>.json from two counter runs
+    of `bench.py --calibrate-copy --no-extra [--config N]` (one counter each): per kernel the mean
+    FETCH_SIZE / WRITE_SIZE over its launches, in KiB, each scaled by what the same counter reads
+    for the 256 MiB device copy (bytes it is known to move)."""
     def load(path, counter):
         vals: dict[str, list[float]] = {}
         with open(path, newline="") as f:
@@ -284,21 +297,24 @@ def summarize_traffic(fetch_csv: str, write_csv: str) -> int:
         return 1
     cf, cw = fetch[copy[0]][0], write[copy[0]][0]
     sf, sw = COPY_KIB / cf, COPY_KIB / cw
-    out = {"workload": "config 2: qkv [64, 240, 1152] h6 d64 non-causal",
+    name, kind, b, h, seq, causal, _, _ = CONFIGS[cfg]
+    out = {"workload": f"{name}: {kind} b{b} h{h} s{seq} d64 "
+                       + ("causal" if causal else "non-causal"),
            "lib_sha256": lib_sha256(), "copy_calibration_kib": COPY_KIB,
            "copy_fetch_kib": round(cf, 1), "copy_write_kib": round(cw, 1),
            "scale_fetch": round(sf, 5), "scale_write": round(sw, 5)}
-    for key, pat in KERNEL_NAMES.items():
-        names = [n for n in fetch if pat in n]
-        if not names:
+    for key, prefix in KERNEL_ROLES:
+        names = [n for n in fetch if _kernel_label(n).startswith(prefix) and n in write]
+        if not names or key in out:
             continue
         fr, wr = statistics.mean(fetch[names[0]]), statistics.mean(write[names[0]])
         fb, wb = round(fr * 1024 * sf), round(wr * 1024 * sw)
-        out[key] = {"fetch_kib_raw": round(fr, 2), "write_kib_raw": round(wr, 2),
+        out[key] = {"kernel": _kernel_label(names[0]), "launches": len(fetch[names[0]]),
+                    "fetch_kib_raw": round(fr, 2), "write_kib_raw": round(wr, 2),
                     "fetch_bytes": fb, "write_bytes": wb, "bytes": fb + wb}
     out["bwd_main_bytes"] = out.get("bwd_main", {}).get("bytes")
     out["fwd_bytes"] = out.get("fwd", {}).get("bytes")
-    TRAFFIC.write_text(json.dumps(out, indent=1) + "\n")
+    traffic_path(cfg).write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out, indent=1))
     return 0
 
@@ -573,6 +589,9 @@ def main() -> int:
     # idling. The line reports the first and last five timed steps, so a ramp shows.
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--causal", action="store_true", help="config 3 as the main workload")
+    ap.add_argument("--config", type=int, choices=sorted(CONFIGS), default=None,
+                    help="the main workload's config (default 2; --causal is config 3); the "
+                         "driver's line is config 2's")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-accuracy", action="store_true", help="skip the fp64 scoring")
     ap.add_argument("--no-extra", action="store_true",
@@ -593,14 +612,15 @@ def main() -> int:
                          "--causal), and "
                          "exit (no GPU)")
     args = ap.parse_args()
+    main_cfg = args.config or (3 if args.causal else 2)
     if args.traffic_from:
-        return summarize_traffic(*args.traffic_from)
+        return summarize_traffic(*args.traffic_from, cfg=main_cfg)
     if args.counters_from:
         return summarize_counters(args.counters_from, max(args.warmup, 1), max(args.steps, 1),
-                                  3 if args.causal else 2)
+                                  main_cfg)
     if args.trace_from:
         return summarize_trace(args.trace_from, max(args.warmup, 1), max(args.steps, 1),
-                               3 if args.causal else 2)
+                               main_cfg)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
               "(the op shards over (batch, head) with no communication; see DESIGN.md)",
@@ -618,7 +638,6 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     L = _lib.lib()
-    main_cfg = 3 if args.causal else 2
     w = Workload(torch, L, _lib, dev, main_cfg)
     B, H, S, D, causal = w.b, w.h, w.s, w.d, w.causal
 

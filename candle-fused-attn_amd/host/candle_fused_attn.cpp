@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <functional>
+#include <map>
 #include <numeric>
 #include <utility>
 
@@ -198,19 +199,68 @@ void WorkspaceCache::give_back(Lease lease) {
 
 // --- Storage, Layout, Tensor -------------------------------------------------------------------
 
-Storage::Storage(std::size_t n, hipStream_t stream) : n_(n), stream_(stream), owned_(true) {
-  if (n > 0) {
-    void* p = nullptr;
-    check_hip(hipMallocFromPoolAsync(&p, n * sizeof(float), device_pool(stream), stream),
-              "allocation");
-    p_ = static_cast<float*>(p);
+// --- device memory: a block cache over the layer's pool --------------------------------------------
+
+namespace {
+
+// Blocks given back by Storage, kept per (stream, size) for the next Storage of that size on that
+// stream: taken and given back with no HIP call and no work on the stream (stream order makes a
+// block's earlier users finish before its next user starts). Only a block of a size not cached
+// comes from the pool (stream-ordered). The stream-ordered calls cost the host about 35 us each,
+// so that at b 64 h 6 s 240 a step's three allocations and frees made the host, not the GPU, set
+// the step's time (0.208 ms per step, the GPU's work 0.190 ms); cached, the host enqueues a step
+// in 0.010 ms.
+std::mutex g_cache_mu;
+std::map<std::pair<hipStream_t, std::size_t>, std::vector<float*>> g_cache;
+
+float* take_block(std::size_t n, hipStream_t stream) {
+  {
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    auto it = g_cache.find({stream, n});
+    if (it != g_cache.end() && !it->second.empty()) {
+      float* p = it->second.back();
+      it->second.pop_back();
+      return p;
+    }
   }
+  void* p = nullptr;
+  check_hip(hipMallocFromPoolAsync(&p, n * sizeof(float), device_pool(stream), stream),
+            "allocation");
+  return static_cast<float*>(p);
+}
+
+void give_block(float* p, std::size_t n, hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(g_cache_mu);
+  g_cache[{stream, n}].push_back(p);
+}
+
+}  // namespace
+
+std::size_t release_cached_blocks() {
+  std::map<std::pair<hipStream_t, std::size_t>, std::vector<float*>> blocks;
+  {
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    blocks.swap(g_cache);
+  }
+  std::size_t n = 0;
+  for (auto& [key, ps] : blocks) {
+    for (float* p : ps) {
+      // Given back to the pool after the work already on the block's stream.
+      check_hip(hipFreeAsync(p, key.first), "release");
+      n += key.second * sizeof(float);
+    }
+  }
+  return n;
+}
+
+Storage::Storage(std::size_t n, hipStream_t stream) : n_(n), stream_(stream), owned_(true) {
+  if (n > 0) p_ = take_block(n, stream);
 }
 
 Storage::Storage(float* external, std::size_t n) : p_(external), n_(n), owned_(false) {}
 
 Storage::~Storage() {
-  if (owned_ && p_) (void)hipFreeAsync(p_, stream_);
+  if (owned_ && p_) give_block(p_, n_, stream_);
 }
 
 std::size_t Layout::elem_count() const {

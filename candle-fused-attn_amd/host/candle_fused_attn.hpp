@@ -11,14 +11,17 @@
 // Layout: start offset, shape, strides, all in f32 elements), the op objects for the nodes candle
 // keeps in its autograd graph, and Error for candle_core::Error.
 //
-// Device memory of outputs, copies and the backward workspace is taken stream-ordered from a memory
-// pool this layer keeps per device (hipMallocFromPoolAsync / hipFreeAsync on the caller's stream):
-// the pool keeps what is given back for later allocations instead of returning it to the driver
-// (a caching allocator, as candle's and torch's are), so a steady-state step allocates nothing
-// from the driver; the memory is held until the process ends. Each op node also keeps its
-// backward workspace between backwards on one stream. Every launch is asynchronous on the
-// caller's stream, so that stream must outlive the tensors allocated on it (their storage is given
-// back on it). There is no CPU path: the operators run on the HIP device only.
+// Device memory of outputs, copies and the backward workspace is cached per stream (a caching
+// allocator, as candle's and torch's are): a tensor's storage, when its last view goes, is kept
+// for the next storage of the same size on the same stream, reused with no HIP call (stream order
+// makes its earlier users finish first); a size not cached comes stream-ordered from a memory pool
+// this layer keeps per device (hipMallocFromPoolAsync). So a steady-state step allocates nothing.
+// The memory is held until the process ends or release_cached_blocks() gives it back; call that
+// before destroying a stream this layer allocated on (its blocks are kept under the stream's
+// handle, which a later stream may reuse). Each op node also keeps its backward workspace between
+// backwards on one stream. Every launch is asynchronous on the caller's stream, so that stream must
+// outlive the tensors allocated on it. There is no CPU path: the operators run on the HIP device
+// only.
 #ifndef CANDLE_FUSED_ATTN_HPP
 #define CANDLE_FUSED_ATTN_HPP
 
@@ -45,11 +48,11 @@ class Error : public std::runtime_error {
   explicit Error(const std::string& msg) : std::runtime_error(msg) {}
 };
 
-// Device memory for f32 values: owned (freed stream-ordered on the stream it was taken on) or a
-// caller's (never freed).
+// Device memory for f32 values: owned (taken from and given back to the layer's cache for the
+// stream it was taken on) or a caller's (never freed).
 class Storage {
  public:
-  Storage(std::size_t n, hipStream_t stream);  // n floats from the layer's pool, stream-ordered
+  Storage(std::size_t n, hipStream_t stream);  // n floats for use on `stream`
   Storage(float* external, std::size_t n);     // wraps memory the caller owns
   ~Storage();
   Storage(const Storage&) = delete;
@@ -63,6 +66,10 @@ class Storage {
   hipStream_t stream_ = nullptr;
   bool owned_ = false;
 };
+
+// Gives the cached device memory back to the layer's pool (stream-ordered, after the work already
+// on each block's stream); returns the bytes given back. Tensors still alive keep theirs.
+std::size_t release_cached_blocks();
 
 // What a candle Layout holds.
 struct Layout {

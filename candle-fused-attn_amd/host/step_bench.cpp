@@ -8,6 +8,7 @@
 // Inputs are ~N(0, 1) (a splitmix64 stream through Box-Muller, seed fixed): the step's time does
 // not depend on the values. Prints one JSON line: the mean ms per step over `steps` back-to-back
 // steps after `warmup` untimed ones, timed by HIP events on the step's stream.
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -79,14 +80,20 @@ int main(int argc, char** argv) {
     check(hipEventCreate(&e1), "event");
     check(hipStreamSynchronize(stream), "sync");
     check(hipEventRecord(e0, stream), "event record");
+    const auto t0 = std::chrono::steady_clock::now();
     for (int i = 0; i < steps; ++i) step();
+    const auto t1 = std::chrono::steady_clock::now();
     check(hipEventRecord(e1, stream), "event record");
     check(hipEventSynchronize(e1), "event sync");
     float ms = 0.0f;
     check(hipEventElapsedTime(&ms, e0, e1), "elapsed time");
-    std::printf("{\"fwd_bwd_ms\": %.5f, \"steps\": %d, \"warmup\": %d, \"b\": %zu, \"h\": %zu, "
-                "\"s\": %zu, \"d\": %zu, \"causal\": %s}\n",
-                ms / steps, steps, warmup, b, h, s, d, causal ? "true" : "false");
+    // The host's time to enqueue a step (the loop returns before the GPU is done unless the host
+    // is the bottleneck).
+    const double host_ms = std::chrono::duration<double, std::milli>(t1 - t0).count() / steps;
+    std::printf("{\"fwd_bwd_ms\": %.5f, \"host_enqueue_ms\": %.5f, \"steps\": %d, "
+                "\"warmup\": %d, \"b\": %zu, \"h\": %zu, \"s\": %zu, \"d\": %zu, "
+                "\"causal\": %s}\n",
+                ms / steps, host_ms, steps, warmup, b, h, s, d, causal ? "true" : "false");
     check(hipEventDestroy(e0), "event");
     check(hipEventDestroy(e1), "event");
   } catch (const cfa::Error& e) {

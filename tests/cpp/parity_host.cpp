@@ -344,6 +344,30 @@ void backward_is_deterministic() {
   }
 }
 
+// The layer's block cache: storage given back is reused for the next storage of that size on the
+// stream (a step in the steady state takes no new memory), release_cached_blocks gives it back,
+// and runs after a release take new blocks and give the same bits.
+void cached_blocks_are_reused_and_released() {
+  const Inputs in = inputs(2, 97, 3, 64);
+  const Run first = run(1, in, false);
+  (void)hipStreamSynchronize(g_stream);
+  const std::size_t released = cfa::release_cached_blocks();
+  expect(released > 0, "a run's freed storage was not cached");
+  const Run again = run(1, in, false);
+  expect(bit_equal(first.o, again.o) && bit_equal(first.dq, again.dq) &&
+             bit_equal(first.dk, again.dk) && bit_equal(first.dv, again.dv),
+         "a run after release_cached_blocks differs");
+  float* a = nullptr;
+  {
+    const cfa::Tensor t = cfa::Tensor::empty({1000}, g_stream);
+    a = t.storage_ptr();
+  }
+  const cfa::Tensor t2 = cfa::Tensor::empty({1000}, g_stream);
+  expect(t2.storage_ptr() == a, "a freed block of the same size on the stream was not reused");
+  const cfa::Tensor t3 = cfa::Tensor::empty({1000}, g_stream);
+  expect(t3.storage_ptr() != a, "a block in use was handed out twice");
+}
+
 // Copy fallbacks (src/lib.rs:110-118, :163-178, :368-380): operands and a gradient the kernels
 // cannot read in place are copied, and the results equal those of aligned operands bit for bit.
 void copy_fallbacks_match_aligned_operands() {
@@ -569,6 +593,7 @@ const Case kCases[] = {
     {"outputs_are_merge_heads_ready", true, outputs_are_merge_heads_ready},
     {"backward_twice_over_one_graph", true, backward_twice_over_one_graph},
     {"backward_is_deterministic", true, backward_is_deterministic},
+    {"cached_blocks_are_reused_and_released", true, cached_blocks_are_reused_and_released},
     {"copy_fallbacks_match_aligned_operands", true, copy_fallbacks_match_aligned_operands},
     {"gradient_views_share_the_qkv_layout", true, gradient_views_share_the_qkv_layout},
     {"strided_copies_match_the_host", true, strided_copies_match_the_host},
