@@ -114,3 +114,72 @@ def test_traffic_summary_and_staleness(tmp_path, monkeypatch):
     monkeypatch.setattr(bench, "lib_sha256", lambda: "bbbb")  # another library: stale
     e = bench.traffic_entry()
     assert e["traffic"] is None and e["traffic_stale_bytes"] == t["bwd_main_bytes"]
+
+
+def write_counter_run(path, w, k, counters):
+    """A counter file of `bench.py --no-extra --warmup w --steps k` (config 2): the dispatch
+    sequence of one run (idle W + K steps, W warm-up, K timed, K forwards, K kernel-level steps, K
+    backwards), each dispatch with `counters(window, kernel)` -> {counter: value}, one row per
+    counter, as rocprofv3 --pmc writes them."""
+    b, h, s = bench.CONFIGS[2][2], bench.CONFIGS[2][3], bench.CONFIGS[2][4]
+    grid = ((s + 127) // 128) * b * h
+    seq = []
+    for win, n, kinds in (("idle", w + k, (FWD, MAIN)), ("warm", w, (FWD, MAIN)),
+                          ("timed", k, (FWD, MAIN)), ("fwds", k, (FWD,)),
+                          ("kern", k, (FWD, MAIN, DQ)), ("bwds", k, (MAIN,))):
+        for _ in range(n):
+            seq += [(win, kind) for kind in kinds]
+    fields = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Workgroup_Size", "Counter_Name",
+              "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    t = 1_000_000
+    with open(path, "w", newline="") as f:
+        wr = csv.DictWriter(f, fieldnames=fields)
+        wr.writeheader()
+        for i, (win, kind) in enumerate(seq):
+            wgs = grid if kind == FWD else (1536 if kind == MAIN else 256)
+            for name, value in counters(win, kind).items():
+                wr.writerow({"Dispatch_Id": i + 1, "Kernel_Name": f"{PREFIX}{kind}(fattn::Args)",
+                             "Grid_Size": wgs * 256, "Workgroup_Size": 256, "Counter_Name": name,
+                             "Counter_Value": value, "Start_Timestamp": t,
+                             "End_Timestamp": t + 100_000})
+            t += 102_000
+
+
+def test_counter_summary_uses_the_timed_window(tmp_path):
+    """`--counters-from`: only the K timed steps' dispatches count (other windows carry other
+    values), passes are merged per kernel, and GRBM_GUI_ACTIVE (summed over the 8 XCDs) is divided
+    by 8: step 2 with 1000 MFMAs (32 cycles each) over 400 GPU-busy cycles x 8 XCDs reads MFMA busy
+    = 32000 / (400 x 1024 SIMDs) = 7.8125 %, 3 other VALU per MFMA, waves per SIMD = 4 x 51200 /
+    (400 x 1024) = 0.5."""
+    w, k = 5, 20
+
+    def pass_a(win, kind):
+        timed = win == "timed"
+        return {"GRBM_GUI_ACTIVE": 3200.0 if timed else 99.0,
+                "SQ_VALU_MFMA_BUSY_CYCLES": 32000.0 if timed else 7.0,
+                "SQ_WAVE_CYCLES": 51200.0 if timed else 5.0}
+
+    def pass_b(win, kind):
+        timed = win == "timed"
+        return {"GRBM_GUI_ACTIVE": 3200.0 if timed else 99.0,
+                "SQ_INSTS_MFMA": 1000.0 if timed else 3.0,
+                "SQ_INSTS_VALU": 4000.0 if timed else 3.0}
+
+    a, b = tmp_path / "a.csv", tmp_path / "b.csv"
+    write_counter_run(a, w, k, pass_a)
+    write_counter_run(b, w, k, pass_b)
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--counters-from", str(a), str(b),
+                        "--warmup", str(w), "--steps", str(k)],
+                       capture_output=True, text=True, check=True)
+    rows = {}
+    for line in r.stdout.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if line.startswith("| ") and len(cells) == 3:
+            rows[cells[0]] = cells[1:]
+    assert rows["dispatches per run"] == [str(k), str(k)]
+    main, fwd = rows["MFMA busy (% of SIMD cycles)"]
+    assert float(main) == pytest.approx(7.8125, rel=1e-3) and float(fwd) == pytest.approx(7.8125,
+                                                                                        rel=1e-3)
+    assert float(rows["other VALU per MFMA"][0]) == pytest.approx(3.0)
+    assert float(rows["waves per SIMD (average)"][0]) == pytest.approx(0.5)
+    assert float(rows["MFMA instruction cycles / MFMA busy cycles"][0]) == pytest.approx(1.0)
