@@ -177,14 +177,27 @@ __device__ __forceinline__ void transpose_groups(f4& x0, f4& x1, f4& x2, f4& x3)
     x3[e] = d;
   }
 }
-// The register operand of the products over head_dim: dst[t] = row[D / 4 g + t] (lane (lo, g)
-// holds quarter g of its row). At D 64 and 128 the row is read in whole 64-byte sectors -- load u
-// of lane group g reads dims 16 u + 4 g .. + 3, so the four groups' loads of one row are 64
-// contiguous bytes -- and 4 x 4 transposes across the lane groups move every float4 to its
-// quarter's group (D 64: one transpose; D 128: one over the even loads, one over the odd). At D 32
-// each lane reads its quarter directly (two float4s). Two phases, so that a caller can issue other
-// memory operations between the loads and the transposes (which wait for the loads): quarter_issue
-// then quarter_place, or load_quarter for both. Every lane of the wave must execute them.
+// The contraction order of the products over head_dim: step t (of D / 4) takes from lane group g
+// the dim quarter_dim(g, t / 4) + t % 4, so each MFMA adds four products, one per group:
+//   D 32: 8 g + t;  D 64: 16 g + t;  D 128: 16 g + t for t < 16, 64 + 16 g + (t - 16) after
+// (D 128 runs D 64's order over each half of the row). Lane (lo, g) reads float4 u of its share of
+// an LDS row at dim quarter_dim(g, u). With 32 g + t at D 128, dK came out 1.6-2.5 x less accurate
+// than the fp32 composed path on the reference tests' closed-form inputs (dP = dO V^T cancels
+// against D there, and that order accumulated it less accurately); by halves it is 0.5-0.9 x, as
+// D 64, and no worse on N(0, 1) inputs.
+template <int D>
+__device__ __forceinline__ constexpr int quarter_dim(int g, int u) {
+  if constexpr (D == 32) return 8 * g + 4 * u;
+  return 64 * (u / 4) + 16 * g + 4 * (u % 4);
+}
+// The register operand of those products: dst[4 u + e] = row[quarter_dim(g, u) + e] (lane (lo, g)
+// holds quarter g of its row, in the order above). At D 64 and 128 the row is read in whole
+// 64-byte sectors -- load u of lane group g reads dims 16 u + 4 g .. + 3, so the four groups' loads
+// of 64 dims are 64 contiguous bytes -- and a 4 x 4 transpose across the lane groups per 64 dims
+// moves every float4 to its group. At D 32 each lane reads its quarter directly (two float4s).
+// Two phases, so that a caller can issue other memory operations between the loads and the
+// transposes (which wait for the loads): quarter_issue then quarter_place, or load_quarter for
+// both. Every lane of the wave must execute them.
 template <int D>
 struct Quarter {
   f4 x[D == 32 ? 2 : D / 16];
@@ -201,27 +214,18 @@ __device__ __forceinline__ void quarter_issue(const float* row, int g, Quarter<D
 }
 template <int D>
 __device__ __forceinline__ void quarter_place(Quarter<D>& q, float (&dst)[D / 4]) {
-  if constexpr (D == 32) {
+  if constexpr (D != 32) {
+    // Before: x[u] of group g holds dims 16 u + 4 g; after, x[4 i + j] holds dims
+    // 64 i + 16 g + 4 j = quarter_dim(g, 4 i + j).
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dst[4 * u + e] = q.x[u][e];
+    for (int i = 0; i < D / 64; ++i) {
+      transpose_groups(q.x[4 * i], q.x[4 * i + 1], q.x[4 * i + 2], q.x[4 * i + 3]);
     }
-  } else {
-    constexpr int kU = D / 16;
-    if constexpr (D == 64) {
-      transpose_groups(q.x[0], q.x[1], q.x[2], q.x[3]);
-    } else {
-      transpose_groups(q.x[0], q.x[2], q.x[4], q.x[6]);
-      transpose_groups(q.x[1], q.x[3], q.x[5], q.x[7]);
-    }
+  }
 #pragma unroll
-    for (int j = 0; j < kU; ++j) {
-      // D 64: x[j] holds dims 16 g + 4 j; D 128: x[2 i] dims 32 g + 4 i, x[2 i + 1] 32 g + 16 + 4 i.
-      const int at = D == 64 ? 4 * j : (j % 2 == 0 ? 2 * j : 16 + 2 * (j - 1));
+  for (int u = 0; u < D / 16; ++u) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dst[at + e] = q.x[j][e];
-    }
+    for (int e = 0; e < 4; ++e) dst[4 * u + e] = q.x[u][e];
   }
 }
 template <int D>
@@ -352,9 +356,9 @@ __device__ __forceinline__ void copy_part_at(const float* base, unsigned row_byt
 // K / V operand read from LDS serving two query tiles; causal QB 64 / KT 32, smaller blocks
 // balancing the triangular work: at b 64 h 6 s 240 causal 42.3 us against 44.1 for KT 48, 42.1 for
 // KT 16, 49.6 for QB 128 / KT 32; at b 8 h 12 s 2048 417.0 against 422.4, 421.0 and 438.5).
-//   S^T = K Q^T per 16-key subtile and column tile n, D / 4 steps: A = K[key 16 mt + lo]
-//   [dim D/4 g + t] (LDS, float4 reads, shared by the column tiles), B = Q[query lo][dim D/4 g + t]
-//   (registers, loaded once). Output: lane (lo, g) holds S[query lo][key 16 mt + 4 g + r].
+//   S^T = K Q^T per 16-key subtile and column tile n, D / 4 steps (the order of quarter_dim):
+//   A = K[key 16 mt + lo][that dim] (LDS, float4 reads, shared by the column tiles),
+//   B = Q[query lo][that dim] (registers, loaded once). Output: lane (lo, g) holds S[query lo][key 16 mt + 4 g + r].
 //   O^T += V^T P^T: M = dims (D / 16 tiles of 16), N = queries, contraction over the tile's keys;
 //   step (kt, r) uses key 16 kt + 4 g + r, i.e. exactly the P value lane (lo, g) holds in its
 //   register (kt, r). A = V[key][dim 16 mt + lo] (LDS, shared by the column tiles).
@@ -436,7 +440,8 @@ fwd_kernel(FwdArgs a) {
   const unsigned k_ss4 = static_cast<unsigned>(a.k.ss) * 4u;
   const unsigned v_ss4 = static_cast<unsigned>(a.v.ss) * 4u;
 
-  // B operands of S^T: Q[qi(n)][D/4 g .. D/4 g + D/4 - 1] for this lane's query in column tile n,
+  // B operands of S^T: quarter g of Q[qi(n)] (quarter_place's order) for this lane's query in
+  // column tile n,
   // negated for a negative scale (so that the raw scores' max is the scaled scores' max).
   const float qsign = a.scale < 0.0f ? -1.0f : 1.0f;
   float qr[kFwdNT][kQR];
@@ -519,7 +524,7 @@ fwd_kernel(FwdArgs a) {
         if (live[mt]) {
 #pragma unroll
           for (int u = 0; u < kQR / 4; ++u) {
-            const f4 kk = ld4(Kt + swz<D>(16 * mt + lo, kQR * g + 4 * u));
+            const f4 kk = ld4(Kt + swz<D>(16 * mt + lo, quarter_dim<D>(g, u)));
 #pragma unroll
             for (int n = 0; n < kCols; ++n) {
               s[n][mt] = mma(kk.x, qr[n][4 * u], s[n][mt]);
@@ -726,8 +731,8 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
 // next tile's Q, dO, L, D in flight during this one (LDS double buffer, filled by direct global ->
 // LDS copies).
 //   S = Q K^T and dP = dO V^T per subtile: M = queries, N = the wave's keys, contraction over the
-//   D dims in D / 4 steps: A = Q / dO [query 16 m + lo][dim D/4 g + t] (LDS, float4 reads),
-//   B = K / V [key lo][dim D/4 g + t].
+//   D dims in D / 4 steps (the order of quarter_dim): A = Q / dO [query 16 m + lo][that dim]
+//   (LDS, float4 reads), B = K / V [key lo][that dim].
 //   P = exp(S scale - L), dS = P o (dP - D), in place in the accumulators.
 //   dV^T += dO^T P, dK^T += Q^T dS: M = dims (D / 16 tiles), N = keys, contraction over the tile's
 //   queries; step (m, r) uses query 16 m + 4 g + r: the P / dS value lane (lo, g) holds in register
@@ -936,7 +941,8 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
                          static_cast<int64_t>(h) * D;
   const unsigned dq_row = 3u * static_cast<unsigned>(a.H) * D;
 
-  // B operands of S and dP: K[key][D/4 g .. D/4 g + D/4 - 1], V likewise; of the dQ product:
+  // B operands of S and dP: quarter g of K[key] (quarter_place's order), V likewise; of the dQ
+  // product:
   // kQ[j][t] = K[k0 + 16 g + t][16 (w + 4 j) + lo]. Zero past S.
   float kB[kKR], vB[kKR], kQ[kKtLds ? 1 : kDQ][16];
   {
@@ -1159,7 +1165,7 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
       if (!live[m]) continue;
 #pragma unroll
       for (int u = 0; u < kKR / 4; ++u) {
-        const int at = swz<D>(16 * m + lo, kKR * g + 4 * u);
+        const int at = swz<D>(16 * m + lo, quarter_dim<D>(g, u));
         const f4 x = ld4(Qt + at), y = ld4(Gt + at);
         sS[m] = mma(x.x, kB[4 * u], sS[m]);
         sS[m] = mma(x.y, kB[4 * u + 1], sS[m]);
@@ -1706,7 +1712,7 @@ __attribute__((amdgpu_waves_per_eu(KG == 1 || D == 32 ? BWD_WAVES : 2))) bwd_spl
     if (live[0]) {
 #pragma unroll
       for (int u = 0; u < kKR / 4; ++u) {
-        const int at = swz<D>(lo, kKR * g + 4 * u);
+        const int at = swz<D>(lo, quarter_dim<D>(g, u));
         const f4 x = ld4(Qt + at), y = ld4(Gt + at);
 #pragma unroll
         for (int c = 0; c < KG; ++c) {

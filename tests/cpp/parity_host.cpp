@@ -167,6 +167,19 @@ double max_rel1(const std::vector<float>& a, const std::vector<float>& r) {
   return m;
 }
 
+// Normwise relative error ||a - r|| / ||r|| (Frobenius norms, in double).
+template <typename A, typename R>
+double rel_fro(const std::vector<A>& a, const std::vector<R>& r) {
+  expect(a.size() == r.size(), "size mismatch");
+  double num = 0, den = 0;
+  for (std::size_t i = 0; i < a.size(); ++i) {
+    const double x = static_cast<double>(r[i]), e = static_cast<double>(a[i]) - x;
+    num += e * e;
+    den += x * x;
+  }
+  return den > 0 ? std::sqrt(num / den) : std::sqrt(num);
+}
+
 bool bit_equal(const std::vector<float>& a, const std::vector<float>& b) {
   return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * sizeof(float)) == 0;
 }
@@ -240,7 +253,10 @@ const char* path_name(int path) { return path == 0 ? "Fused" : "FusedQkv"; }
 
 // tests/parity.rs:147-170: every path against the fp32 oracle at `band` (max-abs on O and the
 // gradients, max_rel1 on L, which the reference does not test); the fp32 oracle's own distance
-// from fp64 printed beside it (the reference's "null band").
+// from fp64 printed beside it (the reference's "null band"). Then against fp64, normwise: O, dQ,
+// dK and dV each within max(2e-6, 1.5 x the fp32 oracle's own normwise error) -- on these
+// closed-form inputs the gradient is ill-conditioned, and the reference's own arithmetic in fp32
+// misses 2e-6 on dQ, so the bar is to be no less accurate than it.
 void check(std::size_t b, std::size_t s, std::size_t h, std::size_t d, bool causal, double band) {
   const Inputs in = inputs(b, s, h, d);
   const double scale = 1.0 / std::sqrt(static_cast<double>(d));
@@ -265,6 +281,19 @@ void check(std::size_t b, std::size_t s, std::size_t h, std::size_t d, bool caus
     expect(eo < band && eg < band && el < band,
            std::string(path_name(path)) + " mismatch: out " + std::to_string(eo) + ", grad " +
                std::to_string(eg) + ", L " + std::to_string(el));
+    const std::vector<float>* got[4] = {&g.o, &g.dq, &g.dk, &g.dv};
+    const std::vector<float>* f32[4] = {&r32.o, &r32.dq, &r32.dk, &r32.dv};
+    const std::vector<double>* f64[4] = {&r64.o, &r64.dq, &r64.dk, &r64.dv};
+    const char* names[4] = {"out", "dq", "dk", "dv"};
+    std::printf("    normwise vs fp64 (bar):");
+    for (int i = 0; i < 4; ++i) {
+      const double e = rel_fro(*got[i], *f64[i]);
+      const double bar = std::max(2e-6, 1.5 * rel_fro(*f32[i], *f64[i]));
+      std::printf(" %s %.2e (%.2e)", names[i], e, bar);
+      expect(e <= bar, std::string(path_name(path)) + " " + names[i] + " normwise " +
+                           std::to_string(e) + " > " + std::to_string(bar));
+    }
+    std::printf("\n");
   }
 }
 

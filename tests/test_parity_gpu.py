@@ -129,6 +129,31 @@ def composed_floor(orc, x, w, h, d, causal, ref_out, ref_grad, scale=None):
     return floor, cmax
 
 
+def check_pairs(orc, qkv, dout, out, grad, h, d, scale, causal, pairs, tag):
+    """The fp64 oracle on chosen (b, h) pairs (index b h + h) of a qkv-path result, for shapes
+    whose every pair would take the oracle minutes: O, dQ, dK, dV of each pair within REL_TOL
+    normwise. qkv, grad [b, s, 3 h d], dout, out [b, s, h d] (device tensors)."""
+    hd = h * d
+
+    def part(t, i, bi, hi):  # pair (bi, hi) of part i as a [1, 1, s, d] host array
+        lo = i * hd + hi * d
+        return t[bi, :, lo:lo + d].cpu().numpy()[None, None]
+
+    for p in pairs:
+        bi, hi = divmod(p, h)
+        q, k, v = (part(qkv, i, bi, hi) for i in range(3))
+        o64, l64 = orc.forward(q, k, v, scale, causal, dtype=np.float64)
+        refs = orc.backward(q, k, v, o64, l64, part(dout, 0, bi, hi), scale, causal,
+                            dtype=np.float64)
+        errs = {"o": orc.rel_fro(part(out, 0, bi, hi), o64)}
+        for i, (name, ref) in enumerate(zip(("dq", "dk", "dv"), refs)):
+            errs[name] = orc.rel_fro(part(grad, i, bi, hi), ref)
+        say(f"  {tag} pair {p} (b {bi}, h {hi}): "
+            + " ".join(f"{k_} {v_:.2e}" for k_, v_ in errs.items()))
+        for k_, v_ in errs.items():
+            assert v_ <= REL_TOL, f"{tag} pair {p}: {k_} normwise error {v_:.3e}"
+
+
 def oracle_qkv(orc, qkv, w, h, d, causal, dtype, scale=None):
     scale = 1.0 / d ** 0.5 if scale is None else scale
     qkv = np.asarray(qkv)
@@ -251,6 +276,26 @@ def test_matches_oracle_closed_form(orc, cuda, shape, causal):
         say(f"  {path}: max-abs vs fp64: out {eo:.2e} grad {eg:.2e}")
         assert max(eo, eg) <= max(BAND, 1.5 * cmax)
     check_lse_all_levels(orc, qkv, h, d, 1.0 / d ** 0.5, causal, "closed form", out)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(2, 7, 3, 32), (1, 97, 2, 32), (2, 7, 3, 128), (1, 97, 2, 128),
+                                   (1, 33, 2, 128), (1, 128, 2, 128), (2, 240, 3, 128)])
+def test_closed_form_other_head_dims(orc, cuda, shape, causal):
+    """The closed-form inputs at head_dim 32 and 128, under the same bars as d 64: no component
+    less accurate than 1.5 x the fp32 composed path's own error against fp64 (or 2e-6). At d 128
+    an earlier contraction order (32 g + t over the whole row) left dK at 1.7-2.5 x the composed
+    path's error and failed here; d 64's order on each half of the row passes with margin."""
+    b, s, h, d = shape
+    say(f"closed form b{b} s{s} h{h} d{d} causal={causal}")
+    x, w = orc.closed_form_inputs(b, s, h, d)
+    ref_out, _, ref_grad = oracle_qkv(orc, x, w, h, d, causal, np.float64)
+    floor, cmax = composed_floor(orc, x, w, h, d, causal, ref_out, ref_grad)
+    qkv, wt = torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda)
+    out, grad = run("fused_qkv", qkv, wt, h, d, causal)
+    check_errors(orc, out, grad, ref_out, ref_grad, f"d{d}", floor, d=d)
+    eg = orc.max_abs(grad.cpu().numpy(), ref_grad)
+    assert eg <= max(zero_band(d), 1.5 * cmax), f"max-abs {eg:.3e}"
 
 
 def test_golden_vectors_gpu(orc, cuda):
@@ -1322,7 +1367,7 @@ def test_very_long_sequence(orc, cuda, causal):
 # --- the split dQ sum by chunks of (b, h) (a workspace that holds some pairs' partials) ---------
 
 @pytest.mark.parametrize("causal,d", [(False, 64), (True, 64), (False, 32)])
-def test_split_by_chunks_matches_whole(cuda, causal, d):
+def test_split_by_chunks_matches_whole(orc, cuda, causal, d):
     """fattn_bwd_f32 with a workspace that holds the split partials of only some (b, h) pairs runs
     steps 2 and 3 per chunk of pairs (causal: equal, 8 | chunk; non-causal: whole rounds of slots), where the chunks are
     large enough to beat the turn hand-over (s 4096: 12 pairs non-causal, 48 causal): the
@@ -1330,7 +1375,8 @@ def test_split_by_chunks_matches_whole(cuda, causal, d):
     the same), and the guard word reads 0. Non-causal b h 24 in chunks of 16 and 8; causal b h 96
     in two of 48; d 32 (128-key blocks, three workgroups per CU) b h 48 in two of 24. A workspace
     whose chunks would be smaller takes the turn hand-over: causal, its gradient equals the
-    split's bit for bit too."""
+    split's bit for bit too. The first pair, one of the last chunk and the last pair are checked
+    against the fp64 oracle."""
     b, h, s = (2, 12, 4096) if not causal else (6, 16, 4096)
     pairs = 16 if not causal else 48
     if d == 32:
@@ -1362,6 +1408,8 @@ def test_split_by_chunks_matches_whole(cuda, causal, d):
     whole_n = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
     whole = backward(whole_n)
     assert torch.isfinite(whole).all()
+    check_pairs(orc, qkv, dout, o, whole, h, d, 0.125, causal, (0, b * h - 3, b * h - 1),
+                f"b{b} h{h} s{s} d{d} causal={causal}")
     n = L.fattn_bwd_workspace_split_bytes(1, pairs, s, d)
     assert n < whole_n
     say(f"chunks of {pairs} (b, h) causal={causal}: workspace {n >> 20} MiB of {whole_n >> 20}")

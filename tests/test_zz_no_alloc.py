@@ -2,8 +2,9 @@
 fattn_bwd_f32 with a caller's workspace of the scratch's size, FATTN_STATIC_SCRATCH_BYTES (so the
 same way of summing dQ: the whole split when it fits, else the split by chunks of (b, h) at
 d <= 64, else turns): bit-identical dQ, dK, dV on two calls in a row, the second on a smaller
-shape, causal and not, and the refusal of a shape whose minimum workspace exceeds the scratch
-(before any launch)."""
+shape, causal and not, the first and last (b, h) pair of every call against the fp64 oracle
+(normwise 2e-6, as every parity test), and the refusal of a shape whose minimum workspace exceeds
+the scratch (before any launch)."""
 from __future__ import annotations
 
 import ctypes
@@ -17,6 +18,7 @@ from candle_fused_attn import _lib
 pytestmark = pytest.mark.gpu
 
 STATIC_SCRATCH = 64 << 20  # FATTN_STATIC_SCRATCH_BYTES (include/fattn.h)
+REL_TOL = 2e-6             # normwise, vs fp64
 
 
 def say(*a):
@@ -29,7 +31,7 @@ def P(t):
 
 def backward_both(b, h, s, d, causal, seed, dev):
     """(dqkv from fattn_bwd_f32_noalloc, dqkv from fattn_bwd_f32 with a workspace of the same
-    kind, the kind) for seeded N(0, 1) qkv and output gradient."""
+    kind, the kind, (qkv, dout, O)) for seeded N(0, 1) qkv and output gradient."""
     L = _lib.lib()
     rng = np.random.default_rng(seed)
     qkv = torch.from_numpy(rng.standard_normal((b, s, 3 * h * d)).astype(np.float32)).to(dev)
@@ -55,11 +57,30 @@ def backward_both(b, h, s, d, causal, seed, dev):
     _lib.check(L.fattn_bwd_f32_noalloc(qp, kp, vp, P(o), P(dout), P(lse), P(got), b, h, s, d,
                                        scale, int(causal), st, st, st, gst, stream))
     torch.cuda.synchronize()
-    return got, want, kind
+    return got, want, kind, (qkv, dout, o)
+
+
+def check_against_oracle(orc, got, io, h, d, causal, pairs):
+    """O and the no-alloc gradient of the (b, h) pairs `pairs` against the fp64 oracle."""
+    qkv, dout, o = io
+    hd, scale = h * d, 1.0 / d ** 0.5
+    for p in pairs:
+        bi, hi = divmod(p, h)
+
+        def part(t, i):  # [1, 1, s, d] host array of pair p, part i
+            return t[bi, :, i * hd + hi * d:i * hd + (hi + 1) * d].cpu().numpy()[None, None]
+
+        q, k, v = (part(qkv, i) for i in range(3))
+        o64, l64 = orc.forward(q, k, v, scale, causal, dtype=np.float64)
+        refs = orc.backward(q, k, v, o64, l64, part(dout, 0), scale, causal, dtype=np.float64)
+        errs = [orc.rel_fro(part(o, 0), o64)]
+        errs += [orc.rel_fro(part(got, i), r) for i, r in enumerate(refs)]
+        say(f"  pair {p}: o dq dk dv " + " ".join(f"{e:.2e}" for e in errs))
+        assert max(errs) <= REL_TOL, (p, errs)
 
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_noalloc_matches_workspace_entry(cuda, causal):
+def test_noalloc_matches_workspace_entry(orc, cuda, causal):
     # (b, h, s, d): split fits the scratch, then a smaller split shape; the config-2 shape (its
     # split workspace exceeds the scratch: split by chunks), then a smaller one; head_dim 32 and
     # 128 (the latter past the scratch: turns).
@@ -70,10 +91,12 @@ def test_noalloc_matches_workspace_entry(cuda, causal):
     for big, small in cases:
         for i, (b, h, s, d) in enumerate((big, small)):
             say(f"noalloc b{b} h{h} s{s} d{d} causal={causal} call {i + 1}")
-            got, want, kind = backward_both(b, h, s, d, causal, seed=b * 1000 + s, dev=cuda)
+            got, want, kind, io = backward_both(b, h, s, d, causal, seed=b * 1000 + s,
+                                                dev=cuda)
             assert torch.isfinite(want).all()
             assert torch.equal(got.view(torch.int32), want.view(torch.int32)), (b, h, s, d, kind)
             say(f"  {kind}: bit-identical")
+            check_against_oracle(orc, got, io, h, d, causal, (0, b * h - 1))
 
 
 def test_noalloc_refuses_what_does_not_fit(cuda):
