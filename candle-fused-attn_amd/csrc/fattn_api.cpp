@@ -591,7 +591,8 @@ int fattn_bwd_f32_noalloc(const float* q, const float* k, const float* v, const 
     return fail(FATTN_EINVAL, "fused_attention: null strides");
   }
   if (int rc = check_range(who, b, h, s, d)) return rc;
-  // The split sum when its workspace fits in the scratch, else the turn hand-over.
+  // dQ summed as fattn_bwd_f32 sums it with a workspace of the scratch's size: the whole split
+  // when it fits, else (d <= 64) the split by chunks of (b, h) pairs, else the turn hand-over.
   const size_t need = fattn::workspace_within(b, h, s, d, FATTN_STATIC_SCRATCH_BYTES);
   if (need > FATTN_STATIC_SCRATCH_BYTES) {
     return fail(FATTN_EWORKSPACE,

@@ -131,8 +131,9 @@ int fattn_bwd_f32(const float* q, const float* k, const float* v, const float* o
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no
  * counterpart in the reference. It calls no allocating routine: the workspace is the library's
  * static scratch, FATTN_STATIC_SCRATCH_BYTES of device memory per GPU, held until the process
- * ends. dQ is summed the split way when that workspace fits in the scratch, else by turns (the
- * same kernels and results as fattn_bwd_f32 with a workspace of that size); a shape whose minimum
+ * ends. dQ is summed as fattn_bwd_f32 sums it with a workspace of that size (the same kernels
+ * and results): the split way when its workspace fits in the scratch, else at d <= 64 split by
+ * chunks of (b, h) pairs where such chunks fit and fill the chip, else by turns; a shape whose minimum
  * workspace exceeds the scratch is refused with FATTN_EWORKSPACE before any launch. Every call on
  * one GPU shares that GPU's scratch: calls that overlap on one GPU (two streams, two threads)
  * race and must be ordered by the caller. */
