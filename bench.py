@@ -60,9 +60,9 @@ SCALE = 0.125
 TRAFFIC = REPO / "profiles" / "traffic.json"
 LIB = REPO / "candle-fused-attn_amd" / "lib" / "libfattn.so"
 COPY_KIB = 256 * 1024            # the --calibrate-copy kernel moves 256 MiB each way
-KERNEL_NAMES = {"fwd": "fwd_kernel<64, 128, 32, 3>", "bwd_main": "bwd_split_kernel<64, 1>",
-                "bwd_dq": "dq_kernel<64>"}
-CAUSAL_FWD_NAME = "fwd_kernel<64, 64, 32, 3>"   # config 3's forward
+KERNEL_NAMES = {"fwd": "fwd_kernel<64, 128, 32, 3, false>",
+                "bwd_main": "bwd_split_kernel<64, 1, false>", "bwd_dq": "dq_kernel<64>"}
+CAUSAL_FWD_NAME = "fwd_kernel<64, 64, 32, 3, true>"   # config 3's forward
 
 # The BASELINE.json configurations this bench times: (name, kind, b, h, s, causal, seed, std).
 CONFIGS = {
@@ -794,7 +794,7 @@ def main() -> int:
                        "step": round(kus["step"], 2)},
         "dq_sum": "split" if w.split else "turns",
         "roofline": {
-            "kernel": ("bwd_split_kernel<64, 1> (fattn_bwd_main_f32_d64, split; its last "
+            "kernel": ("bwd_split_kernel<64, 1, false> (fattn_bwd_main_f32_d64, split; its last "
                        "workgroups sum dQ tiles)" if w.split
                        else "bwd_kernel<false, 64> (fattn_bwd_main_f32_d64, turns)"),
             "bound": "mfma",

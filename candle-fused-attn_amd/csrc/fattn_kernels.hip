@@ -396,9 +396,10 @@ struct FwdArgs {
   int causal;
 };
 
-template <int D, int QB, int KT, int WAVES>
+template <int D, int QB, int KT, int WAVES, bool kCausal>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)))
 fwd_kernel(FwdArgs a) {
+  a.causal = kCausal ? 1 : 0;  // compile-time mask (the host launches the matching instantiation)
   constexpr int kFwdQueries = QB;          // queries per workgroup
   constexpr int kFwdWaveQ = QB / 4;        // queries per wave
   constexpr int kFwdNT = kFwdWaveQ / 16;   // 16-query column tiles per wave
@@ -866,6 +867,8 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   // D always comes from step 1 here (the split mode at D <= 64 runs bwd_split_kernel, which
   // forms D itself).
   static_assert(!kSplit || D == 128, "the split mode at D <= 64 is bwd_split_kernel");
+  // The split instantiations know the mask (kOwnSums is the causal one): every test folds away.
+  if constexpr (kSplit) a.causal = kOwnSums ? 1 : 0;
   __shared__ __attribute__((aligned(16))) float sQ[2][kQT * D];
   __shared__ __attribute__((aligned(16))) float sdO[2][kQT * D];
   // dS [kQT][64 keys], swizzled like a D 64 tile (its writes are column reads' pattern, its
@@ -1507,9 +1510,12 @@ __device__ __forceinline__ void bwd_sum_tiles(const BwdArgs& a, int x, int m, un
   bwd_sum_range<D, kSumTiles>(a, bh, j0, min(a.ntile, j0 + kSumTiles), flag);
 }
 
-template <int D, int KG>
+template <int D, int KG, bool kCausal>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(KG == 1 || D == 32 ? BWD_WAVES : 2))) bwd_split_kernel(BwdArgs a) {
+  // The mask is a compile-time constant of the instantiation (the host launches the one that
+  // matches a.causal): every test of it below folds away (SGPR spills 19 -> 6 / 8 at D 64).
+  a.causal = kCausal ? 1 : 0;
   constexpr int kKeys = kBwdKeys * KG;
   static_assert(D <= 64, "D 128 has no LDS room for three buffers: bwd_kernel<true, 128>");
   static_assert(kNS == 1, "one 16-query subtile per tile");
@@ -1985,7 +1991,16 @@ namespace {
 template <int D, int C>
 const void* fwd_fn() {
   using F = FwdCfg<D, C>;
-  return reinterpret_cast<const void*>(fwd_kernel<D, F::QB, F::KT, F::W>);
+  return reinterpret_cast<const void*>(fwd_kernel<D, F::QB, F::KT, F::W, C != 0>);
+}
+
+// Step 2's split kernel for 64-key (or, `wide`, 128-key) blocks and the mask; causal runs 64-key
+// blocks only (bwd_split_keys), so a wide causal request has no kernel.
+template <int D>
+const void* split_fn(bool wide, bool causal) {
+  if (wide) return causal ? nullptr : reinterpret_cast<const void*>(bwd_split_kernel<D, 2, false>);
+  return causal ? reinterpret_cast<const void*>(bwd_split_kernel<D, 1, true>)
+                : reinterpret_cast<const void*>(bwd_split_kernel<D, 1, false>);
 }
 
 int fwd_qb(int d, int causal) {
@@ -2138,11 +2153,9 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
             g_give_up_bh.load(std::memory_order_relaxed)};
   void* args[] = {&a};
   if (split && d <= 64) {
-    const void* fn = d == 32 ? (kkeys == kBwdKeys
-                                    ? reinterpret_cast<const void*>(bwd_split_kernel<32, 1>)
-                                    : reinterpret_cast<const void*>(bwd_split_kernel<32, 2>))
-                     : kkeys == kBwdKeys ? reinterpret_cast<const void*>(bwd_split_kernel<64, 1>)
-                                         : reinterpret_cast<const void*>(bwd_split_kernel<64, 2>);
+    const bool wide = kkeys != kBwdKeys;
+    const void* fn = d == 32 ? split_fn<32>(wide, causal) : split_fn<64>(wide, causal);
+    if (fn == nullptr) return static_cast<int>(hipErrorInvalidValue);
     return static_cast<int>(launch(fn, nsum ? nmain + nsum : nblk, args, stream));
   }
   // The turn mode at every head_dim; the split mode at 128 (no LDS room for bwd_split_kernel).

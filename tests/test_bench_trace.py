@@ -16,7 +16,7 @@ import pytest  # noqa: E402
 PREFIX = "void fattn::(anonymous namespace)::"
 FWD, MAIN, DQ = (bench.KERNEL_NAMES[k] for k in ("fwd", "bwd_main", "bwd_dq"))
 CAUSAL_FWD = bench.CAUSAL_FWD_NAME
-D32_FWD = "fwd_kernel<32, 128, 64, 3>"
+D32_FWD = "fwd_kernel<32, 128, 64, 3, false>"
 
 
 def write_trace(path, w, k, cfg=2):
