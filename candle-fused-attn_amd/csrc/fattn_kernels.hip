@@ -181,10 +181,10 @@ __device__ __forceinline__ void transpose_groups(f4& x0, f4& x1, f4& x2, f4& x3)
 // the dim quarter_dim(g, t / 4) + t % 4, so each MFMA adds four products, one per group:
 //   D 32: 8 g + t;  D 64: 16 g + t;  D 128: 16 g + t for t < 16, 64 + 16 g + (t - 16) after
 // (D 128 runs D 64's order over each half of the row). Lane (lo, g) reads float4 u of its share of
-// an LDS row at dim quarter_dim(g, u). With 32 g + t at D 128, dK came out 1.6-2.5 x less accurate
+// an LDS row at dim quarter_dim(g, u). With 32 g + t at D 128, dK came out 1.7-2.5 x less accurate
 // than the fp32 composed path on the reference tests' closed-form inputs (dP = dO V^T cancels
-// against D there, and that order accumulated it less accurately); by halves it is 0.5-0.9 x, as
-// D 64, and no worse on N(0, 1) inputs.
+// against D there, and that order accumulated it less accurately); by halves it is 0.6-1.0 x, as
+// at D 64, and no worse on N(0, 1) inputs.
 template <int D>
 __device__ __forceinline__ constexpr int quarter_dim(int g, int u) {
   if constexpr (D == 32) return 8 * g + 4 * u;
@@ -358,7 +358,8 @@ __device__ __forceinline__ void copy_part_at(const float* base, unsigned row_byt
 // KT 16, 49.6 for QB 128 / KT 32; at b 8 h 12 s 2048 417.0 against 422.4, 421.0 and 438.5).
 //   S^T = K Q^T per 16-key subtile and column tile n, D / 4 steps (the order of quarter_dim):
 //   A = K[key 16 mt + lo][that dim] (LDS, float4 reads, shared by the column tiles),
-//   B = Q[query lo][that dim] (registers, loaded once). Output: lane (lo, g) holds S[query lo][key 16 mt + 4 g + r].
+//   B = Q[query lo][that dim] (registers, loaded once). Output: lane (lo, g) holds
+//   S[query lo][key 16 mt + 4 g + r].
 //   O^T += V^T P^T: M = dims (D / 16 tiles of 16), N = queries, contraction over the tile's keys;
 //   step (kt, r) uses key 16 kt + 4 g + r, i.e. exactly the P value lane (lo, g) holds in its
 //   register (kt, r). A = V[key][dim 16 mt + lo] (LDS, shared by the column tiles).
@@ -442,8 +443,8 @@ fwd_kernel(FwdArgs a) {
   const unsigned v_ss4 = static_cast<unsigned>(a.v.ss) * 4u;
 
   // B operands of S^T: quarter g of Q[qi(n)] (quarter_place's order) for this lane's query in
-  // column tile n,
-  // negated for a negative scale (so that the raw scores' max is the scaled scores' max).
+  // column tile n, negated for a negative scale (so that the raw scores' max is the scaled
+  // scores' max).
   const float qsign = a.scale < 0.0f ? -1.0f : 1.0f;
   float qr[kFwdNT][kQR];
   Quarter<D> qload[kFwdNT];  // placed into qr after the first key tile's copies are issued
@@ -945,8 +946,7 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   const unsigned dq_row = 3u * static_cast<unsigned>(a.H) * D;
 
   // B operands of S and dP: quarter g of K[key] (quarter_place's order), V likewise; of the dQ
-  // product:
-  // kQ[j][t] = K[k0 + 16 g + t][16 (w + 4 j) + lo]. Zero past S.
+  // product: kQ[j][t] = K[k0 + 16 g + t][16 (w + 4 j) + lo]. Zero past S.
   float kB[kKR], vB[kKR], kQ[kKtLds ? 1 : kDQ][16];
   {
     const int kr = min(key, S - 1);
