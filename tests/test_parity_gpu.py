@@ -1364,6 +1364,29 @@ def test_very_long_sequence(orc, cuda, causal):
         assert err <= bar, f"{name}: normwise error {err:.3e} > {bar:.3e}"
 
 
+# --- many (b, h) pairs: large grids ----------------------------------------------------------
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_many_pairs(orc, cuda, causal):
+    """b 256 x h 128 = 32768 (b, h) pairs of s 40 through fused_attention_qkv: a forward grid of
+    32768 workgroups, and a step 2 of 32768 key blocks whose dQ sums run in the same launch
+    (non-causal: summing workgroups appended to the grid and planned over the 8 XCDs; causal:
+    each key block sums its own tiles). Sampled pairs (the first, the last, random ones) against
+    the fp64 oracle at 2e-6, and a bit-identical rerun."""
+    b, h, s, d = 256, 128, 40, 64
+    gen = torch.Generator(device=cuda).manual_seed(11 + int(causal))
+    qkv = torch.randn(b, s, 3 * h * d, generator=gen, device=cuda)
+    dout = torch.randn(b, s, h * d, generator=gen, device=cuda)
+    say(f"b {b} h {h} s {s} causal={causal}: {b * h} pairs")
+    out, grad = run("fused_qkv", qkv, dout, h, d, causal, 0.125)
+    _, grad2 = run("fused_qkv", qkv, dout, h, d, causal, 0.125)
+    assert torch.equal(bits(grad), bits(grad2)), "backward reruns differ"
+    rng = np.random.default_rng(5 + int(causal))
+    pairs = sorted({0, b * h - 1, *rng.integers(0, b * h, 10).tolist()})
+    check_pairs(orc, qkv, dout, out, grad, h, d, 0.125, causal, pairs,
+                f"b{b} h{h} s{s} causal={causal}")
+
+
 # --- the split dQ sum by chunks of (b, h) (a workspace that holds some pairs' partials) ---------
 
 @pytest.mark.parametrize("causal,d", [(False, 64), (True, 64), (False, 32)])
