@@ -291,8 +291,9 @@ int run_bwd_prep(const char* who, const float* o, View d_o, void* ws, size_t ws_
   }
   WsParts p{};
   if (int rc = workspace_parts(who, ws, ws_bytes, b, h, s, d, &p)) return rc;
-  // split (d <= 64): step 2 computes D itself and its dQ sums need no clearing (epochs).
-  if (!fattn::bwd_needs_prep(p.part != nullptr, static_cast<int>(d))) return ok();
+  // split (d <= 64, and d 128 with few key blocks per (b, h)): step 2 computes D itself and its
+  // dQ sums need no clearing (epochs).
+  if (!fattn::bwd_needs_prep(p.part != nullptr, static_cast<int>(d), s)) return ok();
   const int err = fattn::launch_bwd_prep(o, d_o, p.dsum, p.turn, p.ctrl, static_cast<int>(b),
                                          static_cast<int>(h), static_cast<int>(s),
                                          static_cast<int>(d), stream);

@@ -203,9 +203,11 @@ int64_t forward_blocks(int64_t b, int64_t h, int64_t s, int causal, int d);
 int64_t bwd_main_blocks(int64_t b, int64_t h, int64_t s);
 int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d);
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s);
-// Whether step 1 (D, counters) must run: the turn mode, and the split mode at d 128 (its step 2
-// has no LDS room to compute D itself).
-bool bwd_needs_prep(bool split, int d);
+// Whether step 1 (D, counters) must run: the turn mode, and the split mode at d 128 past
+// kOwnDMaxBlocks key blocks per (b, h) (fewer: its step 2 forms D itself).
+bool bwd_needs_prep(bool split, int d, int64_t s);
+// D 128, split: step 2 forms D = rowsum(dO o O) itself (few key blocks per (b, h)).
+bool bwd_own_d(int64_t s, int d);
 
 }  // namespace fattn
 

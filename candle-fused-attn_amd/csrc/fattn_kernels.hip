@@ -755,6 +755,7 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const float* __restrict_
 #define BWD_WAVES 3
 #endif
 constexpr int kQT = kBwdQueryTile;
+constexpr int kOwnDMaxBlocks = 4;  // D 128 split: step 2 forms D up to this many key blocks
 constexpr int kNS = kQT / 16;  // 16-query subtiles per tile
 constexpr int kBwdLd = 68;     // pitch (floats) of the transposed K tile at D 128
 // Q and dO tiles are [kQT rows][D floats] in the swizzled layout of swz(), filled by direct copies.
@@ -854,7 +855,7 @@ __device__ __forceinline__ void bwd_sum_range(const BwdArgs& a, int bh, int j0, 
 
 // kOwnSums (split, causal): each key block sums the dQ tiles it completes after its walk; a
 // separate instantiation, so that the non-causal kernel's registers are not spent on it.
-template <bool kSplit, int D, bool kOwnSums = false>
+template <bool kSplit, int D, bool kOwnSums = false, bool kOwnD = false>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArgs a) {
   constexpr int kKR = D / 4;                  // K (or V) values per lane: B operands of S, dP
@@ -865,9 +866,11 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   // fit beside the others.
   constexpr bool kKtLds = D == 128;
   __shared__ __attribute__((aligned(16))) float sKt[kKtLds ? D * kBwdLd : 4];
-  // D always comes from step 1 here (the split mode at D <= 64 runs bwd_split_kernel, which
-  // forms D itself).
   static_assert(!kSplit || D == 128, "the split mode at D <= 64 is bwd_split_kernel");
+  // D = rowsum(dO o O): from step 1, or (kOwnD, split only: few key blocks per (b, h)) formed
+  // here from O rows staged beside dO in one buffer (the two workgroups a CU holds have LDS for
+  // one, not two).
+  static_assert(!kOwnD || kSplit, "D is formed in step 2 in the split mode only");
   // The split instantiations know the mask (kOwnSums is the causal one): every test folds away.
   if constexpr (kSplit) a.causal = kOwnSums ? 1 : 0;
   __shared__ __attribute__((aligned(16))) float sQ[2][kQT * D];
@@ -877,6 +880,7 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   __shared__ __attribute__((aligned(16))) float sdS[kQT * kBwdKeys];
   __shared__ __attribute__((aligned(16))) float sL[2][kQT];
   __shared__ __attribute__((aligned(16))) float sD[2][kQT];
+  __shared__ __attribute__((aligned(16))) float sO[kOwnD ? kQT * D : 4];
   __shared__ int s_item;
   __shared__ unsigned s_flag;  // a dQ sum's poll result (split)
 
@@ -980,21 +984,46 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
 
   // Staging of one query tile, all by direct copies (nothing passes through registers, so no
   // wait is needed before the barrier that precedes the tile): wave w issues copies w, w + 4, ...
-  // of the Q and dO tiles (copy_part); wave 0 copies the tile's L, wave 1 its D (lanes
-  // 0..kQT-1, one float each). Rows past S repeat row S - 1 (finite; masked later).
+  // of the Q and dO tiles (copy_part), and of the O tile where D is formed here; wave 0 copies
+  // the tile's L, wave 1 its D from step 1 (lanes 0..kQT-1, one float each). Rows past S repeat
+  // row S - 1 (finite; masked later).
+  const float* const op = a.o + (static_cast<int64_t>(b) * S * a.H + h) * D;
+  const unsigned o_ss4 = static_cast<unsigned>(a.H) * D * 4u;
   auto gload = [&](int q0, int buf) {
 #pragma unroll
     for (int j0 = 0; j0 < kCopies; j0 += 4) {
       if (j0 + w < kCopies) {
         copy_part<D>(qp, q_ss4, q0, S - 1, sQ[buf], j0 + w, lane);
         copy_part<D>(gp, g_ss4, q0, S - 1, sdO[buf], j0 + w, lane);
+        if constexpr (kOwnD) copy_part<D>(op, o_ss4, q0, S - 1, sO, j0 + w, lane);
       }
     }
-    if (w < 2) {
+    if (kOwnD ? w == 0 : w < 2) {
       if (lane < kQT) {
         const unsigned off = 4u * static_cast<unsigned>(min(q0 + lane, S - 1));
         load_lds4(w == 0 ? lp : dp, off, w == 0 ? sL[buf] : sD[buf]);
       }
+    }
+  };
+  // D of the tile staged in buffer `buf` from its O and dO rows (as step 1: D / 4 lanes per row,
+  // the same operations in the same order).
+  auto form_d = [&](int buf) {
+    constexpr int kLanes = D / 4;
+    // The addresses are recomputed at each call (the empty asm hides that they do not change):
+    // held across the walk, they pushed the kernel's registers past 256.
+    int tv = tid;
+    asm volatile("" : "+v"(tv));
+#pragma unroll
+    for (int i0 = 0; i0 < kQT * kLanes; i0 += kThreads) {
+      const int i = i0 + tv, row = i / kLanes, c4 = i % kLanes;
+      const f4 ov = ld4(&sO[swz<D>(row, 4 * c4)]);
+      const f4 gv = ld4(&sdO[buf][swz<D>(row, 4 * c4)]);
+      float x = ov.x * gv.x;
+      x = fmaf(ov.y, gv.y, x);
+      x = fmaf(ov.z, gv.z, x);
+      x = fmaf(ov.w, gv.w, x);
+      x = lane_sum<kLanes>(x);
+      if (c4 == 0) sD[buf][row] = x;
     }
   };
   // The order in which key blocks add into a tile's dQ (fixed by the shape alone, so every run
@@ -1127,6 +1156,10 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
   gload(tile_at(0) * kQT, 0);
   wait_stores();  // the direct copies have landed
   __syncthreads();
+  if constexpr (kOwnD) {
+    form_d(0);
+    __syncthreads();
+  }
   // One tile; `bufc()` is the LDS buffer, t % 2. The split kernel unrolls the walk by two so that
   // it is a compile-time constant there and LDS addresses fold the buffer offset into the
   // instruction (the turn kernel has no registers to spare for that).
@@ -1287,6 +1320,11 @@ __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : BWD_WAVES))) bwd_kernel(BwdArg
     p1_q0 = q0;
     p1_pos = pos_of(q0 / kQT);
     p1_cnt = count_of(q0 / kQT);
+    // D of the next tile (its O and dO rows landed before the barrier above; the O buffer is
+    // refilled only after the barrier below).
+    if constexpr (kOwnD) {
+      if (has_next) form_d(buf ^ 1);
+    }
     __syncthreads();  // dS read by every wave
   };
   if constexpr (kSplit) {
@@ -2033,7 +2071,16 @@ int64_t bwd_prep_blocks(int64_t b, int64_t h, int64_t s, int d) {
   return (b * h * s + rows_per_block - 1) / rows_per_block;
 }
 int64_t bwd_dq_blocks(int64_t b, int64_t h, int64_t s) { return b * h * ((s + kQT - 1) / kQT); }
-bool bwd_needs_prep(bool split, int d) { return !split || d > 64; }
+bool bwd_own_d(int64_t s, int d) {
+  // D 128 split: step 2 forms D itself up to kOwnDMaxBlocks key blocks per (b, h), where every
+  // key block re-forming D for its tiles costs less than step 1's launch and pass over O and dO.
+  // Measured (backward, A/B in one process): b 64 h 6 s 240 320.9 -> 314.7 us, causal 230.4 ->
+  // 228.9; but b 8 h 12 s 2048 causal 2334 -> 2490 and b 16 h 16 s 1024 3052 -> 3186.
+  return d == 128 && (s + kBwdKeys - 1) / kBwdKeys <= kOwnDMaxBlocks;
+}
+bool bwd_needs_prep(bool split, int d, int64_t s) {
+  return !split || (d > 64 && !bwd_own_d(s, d));
+}
 namespace {
 std::atomic<int> g_step2_sums{1};
 std::atomic<int> g_sum_shift{0};
@@ -2159,13 +2206,16 @@ int launch_bwd_main(View q, View k, View v, View d_o, const float* o, const floa
     return static_cast<int>(launch(fn, nsum ? nmain + nsum : nblk, args, stream));
   }
   // The turn mode at every head_dim; the split mode at 128 (no LDS room for bwd_split_kernel).
+  const bool own_d = split && bwd_own_d(s, d);
   const void* fn;
   if (d == 32) {
     fn = reinterpret_cast<const void*>(bwd_kernel<false, 32>);
   } else if (d == 128) {
     fn = !split  ? reinterpret_cast<const void*>(bwd_kernel<false, 128>)
-         : causal ? reinterpret_cast<const void*>(bwd_kernel<true, 128, true>)
-                  : reinterpret_cast<const void*>(bwd_kernel<true, 128>);
+         : causal ? (own_d ? reinterpret_cast<const void*>(bwd_kernel<true, 128, true, true>)
+                           : reinterpret_cast<const void*>(bwd_kernel<true, 128, true>))
+                  : (own_d ? reinterpret_cast<const void*>(bwd_kernel<true, 128, false, true>)
+                           : reinterpret_cast<const void*>(bwd_kernel<true, 128>));
   } else {
     fn = reinterpret_cast<const void*>(bwd_kernel<false, 64>);
   }
