@@ -88,8 +88,9 @@ size_t fattn_bwd_workspace_split_bytes(int64_t b, int64_t h, int64_t s, int64_t 
 
 /* Backward step 1: D[b, h, i] = sum_c dO[b, i, h, c] * O[b, i, h, c] (fixed order) and the
  * counters of step 2 cleared. O is [b, s, h, d] contiguous; dO is read through do_strides. With
- * a split-size workspace at d <= 64 there is nothing to do (step 2 computes D itself, and tags
- * the state of its own dQ sums with a value unique to its launch; returns 0 after the checks).
+ * a split-size workspace at d <= 64, and at d 128 with s <= 256, there is nothing to do (step 2
+ * computes D itself, and tags the state of its own dQ sums with a value unique to its launch;
+ * returns 0 after the checks).
  * Replaces the fattn_bwd_dot_f32_d64 launch (src/cuda.rs:215-231). */
 int fattn_bwd_prep_f32(const float* o, const float* d_o, const int64_t do_strides[3],
                        void* workspace, size_t workspace_bytes, int64_t b, int64_t h, int64_t s,
