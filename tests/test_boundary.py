@@ -314,6 +314,19 @@ def test_step1_grid_uses_64_bit_thread_indices():
     assert "exceeds i32 indexing" in _lib.last_error()
 
 
+def test_step1_is_a_no_op_where_step2_forms_d():
+    """With a split-size workspace step 2 forms D = rowsum(dO o O) itself at d <= 64, and at d 128
+    up to four 64-key blocks per (b, h) (s <= 256): fattn_bwd_prep_f32 then returns 0 after its
+    checks, without a launch (so it runs here, with no device and pointers never dereferenced)."""
+    L = _lib.lib()
+    for b, h, s, d in ((2, 3, 240, 64), (2, 3, 240, 32), (2, 3, 240, 128), (1, 2, 256, 128),
+                       (1, 1, 1, 128)):
+        st = a3(s * h * d, d, h * d)
+        n = L.fattn_bwd_workspace_split_bytes(b, h, s, d)
+        rc = L.fattn_bwd_prep_f32(BAD, BAD, st, BAD, n, b, h, s, d, None)
+        assert rc == 0, (b, h, s, d, _lib.last_error())
+
+
 def sum_audit(b, h, s, d, causal):
     L = _lib.lib()
     f = L.fattn_internal_sum_audit
