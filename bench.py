@@ -529,11 +529,21 @@ def summarize_counters(csvs: list[str], warmup: int, steps: int, cfg: int = 2) -
     return 0
 
 
-def time_extra(torch, w: Workload, steps: int, warmup: int) -> dict:
+def time_extra(torch, w: Workload, steps: int, warmup: int, warm_ms: float = 200.0) -> dict:
     """Op-level forward, backward and forward+backward ms, and each kernel's us, of one extra
-    config."""
+    config, after at least `warmup` steps and at least `warm_ms` of back-to-back steps: the first
+    calls on a new shape touch freshly allocated pages, and MI355X raises its clocks over some
+    tens of milliseconds of sustained work (100 steps of config 3 are 14 ms, right after the
+    headline's steps from idle)."""
     for _ in range(warmup):
         w.step()
+    torch.cuda.synchronize()
+    done, t0 = warmup, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(20):
+            w.step()
+        torch.cuda.synchronize()
+        done += 20
     fb_ms, _, _ = event_steps(torch, w.stream, w.step, steps)
     f_ms, _, _ = event_steps(torch, w.stream, w.fwd, steps)
     kus = kernel_steps(torch, w.stream, w.kernels, steps)
@@ -553,7 +563,7 @@ def time_extra(torch, w: Workload, steps: int, warmup: int) -> dict:
         "bwd_steps_frac": round(f_bwd / (bwd_us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
         "fwd_kernel_frac": round(f_fwd / (kus["fwd"] * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
         "dq_sum": "split" if w.split else "turns",
-        "steps": steps, "warmup": warmup,
+        "steps": steps, "warmup": done,
     }
 
 
@@ -671,8 +681,6 @@ def main() -> int:
             if cfg == main_cfg:
                 continue
             xw = Workload(torch, L, _lib, dev, cfg)
-            # 100 warm-up steps: the first calls on a new shape touch freshly allocated pages,
-            # and config 3's steps (0.16 ms) would otherwise run while the clocks still rise.
             extra[f"config{cfg}"] = time_extra(torch, xw, max(args.extra_steps, 1), 100)
             log(f"bench: {CONFIGS[cfg][0]}: {json.dumps(extra[f'config{cfg}'])}")
             del xw
